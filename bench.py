@@ -1,0 +1,401 @@
+#!/usr/bin/env python3
+"""int4 dequant + GEMM benchmark on one MI355X.
+
+Headline (``value``): packed-weight GB/s of the act-order decode sweep at
+M=1 - one step = one GEMV over each of the (K, N) shapes (5120,5120),
+(5120,17408), (17408,5120), (5120,1024), GPTQ v1, groupsize 32, act-order
+g_idx, bf16 activations. Weight copies are rotated so every step streams
+more distinct weight bytes than the 256 MB Infinity Cache holds.
+
+``sub_results`` time the other workloads (decode M=8, M=16 gs32, M=4096 v2
+DiT shapes, odd groupsize 26, RTN linear, RTN embedding, 64-expert MoE).
+``roofline`` is the dominant kernel (the split-K GEMV at K=5120, N=17408,
+M=1) timed with HIP events on the launch stream. ``cpu_baseline`` times the
+CPU oracle (numpy restatement of the reference's packed path) on one pass of
+the M=1 sweep.
+
+    python bench.py [--steps K] [--warmup W] [--workloads all|decode,...]
+"""
+from __future__ import annotations
+
+import argparse
+import copy
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "onecompression-runtime_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "int4 GEMM TFLOP/s & weight GB/s at M=1/16/4096; % of MI355X roofline"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+DECODE_SHAPES = [(5120, 5120), (5120, 17408), (17408, 5120), (5120, 1024)]
+DIT_SHAPES = [(3072, 3072), (3072, 12288), (12288, 3072)]
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gptq_bytes(K: int, N: int, gs: int = 32) -> int:
+    """qweight + fp16 scales + qzeros of a GPTQ layer (0.578125 B/weight at gs 32)."""
+    G = math.ceil(K / gs)
+    return (math.ceil(K / 8) * N * 4) + G * N * 2 + G * (N // 8) * 4
+
+
+def time_ms(launch, iters: int, warmup: int) -> float:
+    """Average ms per call of ``launch(i)`` between two HIP events on the current stream."""
+    import torch
+
+    for i in range(warmup):
+        launch(i)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(iters):
+        launch(i)
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def build_gptq(K, N, *, seed, dev, copies, **kw):
+    """One module per weight copy (distinct device memory), same values."""
+    import torch
+
+    from onecomp_runtime import backend, synthetic
+
+    layer = synthetic.gptq_layer(K, N, seed=seed, **kw)
+    entry = dict(in_features=K, out_features=N, wbits=4, groupsize=layer.groupsize,
+                 actorder=layer.g_idx is not None, checkpoint_format="gptq" if layer.v1 else "gptq_v2",
+                 name="bench")
+    st = dict(qweight=layer.qweight, scales=layer.scales, qzeros=layer.qzeros)
+    if layer.g_idx is not None:
+        st["g_idx"] = layer.g_idx
+    mod, _ = backend.build_quant_layer(entry, st, "hip", torch.bfloat16, dev)
+    mods = [mod] + [copy.deepcopy(mod) for _ in range(copies - 1)]
+    return layer, mods
+
+
+def decode_workload(dev, M, steps, warmup, layers_cache):
+    """The act-order decode sweep at one M; returns (result dict, per-shape data)."""
+    import torch
+
+    from onecomp_runtime import synthetic
+
+    per_copy = sum(gptq_bytes(K, N) for K, N in DECODE_SHAPES)
+    copies = max(2, math.ceil(2 * MALL_BYTES / per_copy))
+    if "decode" not in layers_cache:
+        built = []
+        for i, (K, N) in enumerate(DECODE_SHAPES):
+            log(f"building decode layer K={K} N={N} x{copies}")
+            built.append(build_gptq(K, N, seed=20270 + i, dev=dev, copies=copies, act_order=True))
+        layers_cache["decode"] = built
+    built = layers_cache["decode"]
+    xs = [synthetic.activations(M, K, seed=20271 + M).to(dev) for K, _ in DECODE_SHAPES]
+
+    def step(i):
+        c = i % copies
+        for (layer, mods), x in zip(built, xs):
+            mods[c](x)
+
+    with torch.no_grad():
+        ms = time_ms(step, steps, warmup)
+    wbytes = sum(gptq_bytes(K, N) for K, N in DECODE_SHAPES)
+    flops = sum(2 * M * K * N for K, N in DECODE_SHAPES)
+    res = {
+        "ms_per_step": ms,
+        "weight_GBps": wbytes / (ms * 1e-3) / 1e9,
+        "TFLOPs": flops / (ms * 1e-3) / 1e12,
+        "hbm_frac": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "rotation_bytes": per_copy * copies,
+    }
+    return res, built, xs, copies
+
+
+def dominant_kernel(dev, built, xs, copies, iters):
+    """Split-K GEMV at K=5120, N=17408, M=1, timed alone (events over the region)."""
+    import torch
+
+    idx = DECODE_SHAPES.index((5120, 17408))
+    _, mods = built[idx]
+    x = xs[idx]
+    with torch.no_grad():
+        ms = time_ms(lambda i: mods[i % copies](x), iters, 10)
+    K, N = DECODE_SHAPES[idx]
+    M = x.shape[0]
+    algo = gptq_bytes(K, N) + K * 4 + M * K * 2 + M * N * 2  # + kmap, activations, output
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_splitk_kernel<bf16,f16,MT=1,kmap>", "shape": f"M={M} K={K} N={N}",
+            "launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": algo}
+
+
+def gptq_m16_workload(dev, steps, warmup):
+    import torch
+
+    from onecomp_runtime import synthetic
+
+    K = N = 4096
+    copies = math.ceil(2 * MALL_BYTES / gptq_bytes(K, N))
+    log(f"building gptq_gs32 layer x{copies}")
+    _, mods = build_gptq(K, N, seed=20260, dev=dev, copies=copies)
+    x = synthetic.activations(16, K, seed=20261).to(dev)
+    with torch.no_grad():
+        ms = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+    gbps = gptq_bytes(K, N) / (ms * 1e-3) / 1e9
+    return {"M": 16, "K": K, "N": N, "us": ms * 1e3, "weight_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBS,
+            "TFLOPs": 2 * 16 * K * N / (ms * 1e-3) / 1e12}
+
+
+def dit_workload(dev, steps, warmup):
+    import torch
+
+    from onecomp_runtime import synthetic
+
+    out = {}
+    tot_flops = tot_ms = 0.0
+    for i, (K, N) in enumerate(DIT_SHAPES):
+        log(f"building dit layer K={K} N={N}")
+        _, mods = build_gptq(K, N, seed=20280 + i, dev=dev, copies=1, v1=False)
+        x = synthetic.activations(4096, K, seed=20281, outliers=True).to(dev)
+        with torch.no_grad():
+            ms = time_ms(lambda j: mods[0](x), steps, warmup)
+        flops = 2 * 4096 * K * N
+        tf = flops / (ms * 1e-3) / 1e12
+        out[f"K{K}_N{N}"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+        tot_flops += flops
+        tot_ms += ms
+        del mods, x
+    tf = tot_flops / (tot_ms * 1e-3) / 1e12
+    out["aggregate"] = {"TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+    return out
+
+
+def padded_workload(dev, steps, warmup):
+    import torch
+
+    from onecomp_runtime import synthetic
+
+    K, N, M = 1040, 3072, 256
+    copies = math.ceil(2 * MALL_BYTES / gptq_bytes(1056, N))
+    _, mods = build_gptq(K, N, seed=20290, dev=dev, copies=copies, groupsize=26, pad_rows_to=1056)
+    x = synthetic.activations(M, K, seed=20291).to(dev)
+    with torch.no_grad():
+        ms = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+    tf = 2 * M * K * N / (ms * 1e-3) / 1e12
+    wb = 1056 // 8 * N * 4 + 40 * N * 2 + 40 * N // 8 * 4
+    return {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
+            "GBps": (wb + M * K * 2 + M * N * 2) / (ms * 1e-3) / 1e9}
+
+
+def rtn_workload(dev, steps, warmup):
+    import torch
+
+    from onecomp_runtime import PackedEmbedding, PackedRTNLinear, synthetic
+
+    res = {}
+    M, K, N = 512, 1024, 2048
+    layer = synthetic.rtn_layer(N, K, seed=20300)
+    mod = PackedRTNLinear(K, N, layer.qweight_u8.to(dev), layer.scales.to(dev), layer.zeros.to(dev))
+    x = synthetic.activations(M, K, seed=20301).to(dev)
+    with torch.no_grad():
+        ms = time_ms(lambda i: mod(x), steps * 4, warmup)
+    tf = 2 * M * K * N / (ms * 1e-3) / 1e12
+    res["rtn_linear_m512"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+    V, D, T = 32768, 1024, 4096
+    for G in (1, 32):
+        emb_layer = synthetic.rtn_layer(V, D, seed=20310, groups=G)
+        emb = PackedEmbedding(V, D, emb_layer.qweight_u8.to(dev), emb_layer.scales.to(dev),
+                              emb_layer.zeros.to(dev))
+        ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311)).to(dev)
+        with torch.no_grad():
+            ms = time_ms(lambda i: emb(ids), steps * 4, warmup)
+        nbytes = T * (D // 2 + 4 * G) + T * 8 + T * D * 2
+        res[f"rtn_embedding_G{G}"] = {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
+                                      "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+    return res
+
+
+def moe_workload(dev, steps, warmup):
+    import torch
+
+    from onecomp_runtime import kernels, synthetic
+
+    E, K, N, T, topk = 64, 4096, 2048, 512, 8
+    log("building 64 experts")
+    experts = synthetic.moe_experts(E, K, N, seed=20330, keep_codes=False)
+    copies = 2
+    w = [(experts.qweight.to(dev), experts.scales.to(dev), experts.qzeros.to(dev))]
+    w.append(tuple(t.clone() for t in w[0]))
+    x = synthetic.activations(T, K, seed=20331).to(dev)
+    ids = synthetic.router_topk(T, E, topk, seed=20332).to(dev)
+
+    def step(i):
+        off, pairs = kernels.moe_route(ids, E)
+        qw, sc, qz = w[i % copies]
+        kernels.int4_moe_gemm(x, topk, qw, sc, qz, off, pairs)
+
+    with torch.no_grad():
+        ms = time_ms(step, steps, warmup)
+    wbytes = E * gptq_bytes(K, N)
+    flops = 2 * T * topk * K * N
+    return {"us": ms * 1e3, "weight_GBps": wbytes / (ms * 1e-3) / 1e9,
+            "hbm_frac": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "TFLOPs": flops / (ms * 1e-3) / 1e12}
+
+
+def cpu_baseline(budget_s: float):
+    """Oracle packed path (numpy dequant + fp32 GEMM) on the M=1 decode sweep,
+    column chunks spread over a thread pool of the host's cores."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import numpy as np
+
+    from onecomp_runtime import synthetic
+    from oracle import onecomp_oracle as O
+
+    cores = min(16, os.cpu_count() or 1)
+    layers = []
+    for i, (K, N) in enumerate(DECODE_SHAPES):
+        layer = synthetic.gptq_layer(K, N, seed=20270 + i, act_order=True)
+        x = synthetic.activations(1, K, seed=20272).float().numpy()
+        layers.append((K, N, layer.qweight.numpy(), layer.scales.float().numpy(), layer.qzeros.numpy(),
+                       layer.g_idx.numpy(), x))
+        del layer
+
+    def run_chunk(args):
+        K, qw, sc, qz, g, x, n0, n1 = args
+        n8 = slice(n0 // 8, n1 // 8)
+        return O.gptq_linear(x, qw[:, n0:n1], sc[:, n0:n1], qz[:, n8], g, K, n1 - n0, "bf16")
+
+    def one_pass(pool):
+        for K, N, qw, sc, qz, g, x in layers:
+            step = max(8, (N // cores) // 8 * 8)
+            chunks = [(K, qw, sc, qz, g, x, n0, min(N, n0 + step)) for n0 in range(0, N, step)]
+            np.concatenate(list(pool.map(run_chunk, chunks)), axis=1)
+
+    with ThreadPoolExecutor(cores) as pool:
+        one_pass(pool)  # warm
+        t0 = time.perf_counter()
+        passes = 0
+        while True:
+            one_pass(pool)
+            passes += 1
+            if time.perf_counter() - t0 > budget_s / 2 or passes >= 5:
+                break
+        dt = (time.perf_counter() - t0) / passes
+    wbytes = sum(gptq_bytes(K, N) for K, N in DECODE_SHAPES)
+    return {"value": round(wbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+            "sample": f"{passes} pass(es) of the M=1 act-order decode sweep (4 shapes, "
+                      f"{wbytes/1e6:.0f} MB packed weights): oracle packed path, numpy dequant + "
+                      f"fp32 GEMM per call, {cores} threads over column chunks; {dt*1e3:.0f} ms/pass"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workloads", default="all",
+                    help="comma list of: m16,dit,padded,rtn,moe (the headline always runs)")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE={world}); "
+              "this workload does not shard across GPUs in this build", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = {"m16", "dit", "padded", "rtn", "moe"} if args.workloads == "all" else set(args.workloads.split(","))
+
+    cache: dict = {}
+    log("decode sweep M=1 (headline)")
+    head, built, xs, copies = decode_workload(dev, 1, args.steps, args.warmup, cache)
+    log(f"headline {head['weight_GBps']:.1f} GB/s, {head['ms_per_step']*1e3:.1f} us/step")
+    roof = dominant_kernel(dev, built, xs, copies, max(100, args.steps * 4))
+    log(f"dominant kernel {roof['achieved']} GB/s ({roof['launch_us']} us/launch)")
+    sub = {}
+    m8, _, _, _ = decode_workload(dev, 8, args.steps, args.warmup, cache)
+    sub["decode_actorder_m8"] = m8
+    per_shape = {}
+    for (K, N), (layer, mods), x in zip(DECODE_SHAPES, built, xs):
+        with torch.no_grad():
+            ms = time_ms(lambda i: mods[i % copies](x), args.steps * 2, args.warmup)
+        per_shape[f"K{K}_N{N}"] = {"us": ms * 1e3, "weight_GBps": gptq_bytes(K, N) / (ms * 1e-3) / 1e9}
+    sub["decode_actorder_m1_per_shape"] = per_shape
+    del built, xs, cache
+    torch.cuda.empty_cache()
+    if "m16" in wl:
+        log("gptq_gs32 M=16")
+        sub["gptq_gs32_m16"] = gptq_m16_workload(dev, args.steps, args.warmup)
+    if "dit" in wl:
+        log("dit M=4096")
+        sub["dit_large_m_m4096"] = dit_workload(dev, max(5, args.steps // 5), 3)
+    if "padded" in wl:
+        log("padded gs26")
+        sub["padded_gs26_m256"] = padded_workload(dev, args.steps, args.warmup)
+    if "rtn" in wl:
+        log("rtn linear / embedding")
+        sub.update(rtn_workload(dev, args.steps, args.warmup))
+    if "moe" in wl:
+        log("moe")
+        sub["moe_64x_top8"] = moe_workload(dev, max(5, args.steps // 2), 3)
+    torch.cuda.synchronize()
+
+    cpu = None
+    if not args.no_cpu:
+        log("cpu baseline (oracle)")
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    def rnd(o):
+        if isinstance(o, float):
+            return round(o, 4)
+        if isinstance(o, dict):
+            return {k: rnd(v) for k, v in o.items()}
+        return o
+
+    line = {
+        "metric": METRIC,
+        "value": round(head["weight_GBps"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["ms_per_step"], 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "decode_actorder_m1", "M": 1, "shapes_KN": DECODE_SHAPES, "groupsize": 32,
+                   "act_order": True, "format": "gptq (v1 zeros)", "activations": "bf16",
+                   "weight_rotation_bytes": head["rotation_bytes"],
+                   "value_bytes": "packed qweight+scales+qzeros per step"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "hbm_frac_step": round(head["hbm_frac"], 4),
+        "sub_results": rnd(sub),
+        "device": torch.cuda.get_device_name(dev),
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

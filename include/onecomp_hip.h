@@ -1,0 +1,237 @@
+/*
+ * onecomp_hip.h - C ABI of the MI355X (gfx950) int4 dequant + GEMM library
+ * (libonecomp_hip.so).
+ *
+ * Every entry point is `extern "C"`, takes plain device pointers, element
+ * counts and a HIP stream passed as `void*` (a hipStream_t; NULL = the legacy
+ * default stream), never allocates user tensors, launches asynchronously on
+ * that stream and returns an `int` status (OC_OK on success). A failed call
+ * leaves a human-readable reason in oc_last_error() (thread-local).
+ *
+ * Layouts follow the reference's AutoGPTQ / RTN checkpoint formats:
+ *   qweight  int32 [ceil(K/8), N]  8 nibbles per word, packed along K:
+ *            code(k, n) = (qweight[k/8][n] >> (4*(k%8))) & 0xF
+ *   qzeros   int32 [G, N/8]        8 nibbles per word, packed along N:
+ *            zst(g, n) = (qzeros[g][n/8] >> (4*(n%8))) & 0xF
+ *            V1 ("gptq")    zero = (zst + 1) & 0xF
+ *            V2 ("gptq_v2") zero = zst
+ *   scales   fp16/bf16 [G, N]
+ *   RTN      uint8 [rows, ceil(K/2)]  byte j holds col 2j (low nibble) and
+ *            col 2j+1 (high nibble); scales/zeros [rows, G] (G = 1: per row)
+ *
+ * Reference citations are relative to the onecompression-runtime source tree.
+ */
+#ifndef ONECOMP_HIP_H
+#define ONECOMP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define OC_OK 0
+#define OC_ERR_INVALID_ARGUMENT 1 /* bad pointer / dtype / flag            */
+#define OC_ERR_SHAPE 2            /* shape or alignment contract violated  */
+#define OC_ERR_UNSUPPORTED 3      /* valid but not implemented here        */
+#define OC_ERR_WORKSPACE 4        /* workspace missing or too small        */
+#define OC_ERR_HIP 5              /* a HIP runtime call failed             */
+
+/* ---- element types ----------------------------------------------------- */
+#define OC_DTYPE_F16 1
+#define OC_DTYPE_BF16 2
+#define OC_DTYPE_F32 3
+#define OC_DTYPE_U8 4
+#define OC_DTYPE_I32 5
+
+/* ---- zero-point conventions -------------------------------------------- */
+#define OC_ZERO_V1 1 /* stored zero-1, restored as (z+1)&0xF (format "gptq")  */
+#define OC_ZERO_V2 2 /* stored zero as is (format "gptq_v2")                 */
+
+/* ---- GEMM regime selection (oc_int4_gemm `regime`) ---------------------- */
+#define OC_REGIME_AUTO 0
+#define OC_REGIME_SPLITK 1 /* small-M split-K streaming kernel (M <= 64)     */
+#define OC_REGIME_TILED 2  /* large-M LDS-tiled MFMA kernel                  */
+
+/* Human-readable name of a status code. */
+const char *oc_status_string(int status);
+
+/* Detail message of the last failed call on this thread ("" if none). */
+const char *oc_last_error(void);
+
+/* ABI version (major*10000 + minor*100 + patch). */
+int oc_version(void);
+
+/*
+ * Host-only (no GPU needed): plan the physical row layout that turns any
+ * GPTQ grouping into uniform groups of `group_rows` rows (a multiple of 32).
+ *
+ * Group g's input columns (k with g(k) == g, ascending k) occupy physical
+ * rows [g*group_rows, g*group_rows + count_g); the remaining rows of the
+ * slot are zero rows (kmap = -1). g(k) = g_idx[k] when g_idx != NULL
+ * (act-order), else k / groupsize. This single re-layout covers
+ *   - act-order g_idx (replaces the per-call `scales[g_idx]` gather of
+ *     quant_utils.py:66-67 by a load-time row permutation),
+ *   - odd group sizes < 32 (the reference's _repack_groups_to_32,
+ *     layers/fused_int4_linear.py:94-124, and its activation remap at
+ *     :370-376),
+ *   - K not a multiple of the group size (K padding, :989-1045).
+ * Outputs: kmap_out[K_phys] (activation column of each physical row, -1 for
+ * a zero row), *k_phys_out, *group_rows_out, *num_groups_out, and
+ * *identity_out = 1 when kmap is the identity (kmap[k] == k, K_phys == K),
+ * in which case the GEMM may be called with kmap = NULL.
+ * If kmap_out is NULL only the sizes are returned (query mode).
+ */
+int oc_int4_plan_groups(const int64_t *g_idx, int32_t K, int32_t groupsize,
+                        int32_t *kmap_out, int64_t kmap_capacity,
+                        int32_t *k_phys_out, int32_t *group_rows_out,
+                        int32_t *num_groups_out, int32_t *identity_out);
+
+/*
+ * Device: re-lay packed rows. Physical row k' of qweight_out [K_phys/8, N]
+ * takes the 4-bit code of input row kmap[k'] (zero code when kmap[k'] < 0).
+ * Replaces the load-time repacks at layers/fused_int4_linear.py:76-124 and
+ * the K padding at :1016-1045. qweight_in is [ceil(K/8), N].
+ */
+int oc_int4_repack_rows(const int32_t *qweight_in, int32_t K, int32_t N,
+                        const int32_t *kmap, int32_t K_phys,
+                        int32_t *qweight_out, void *stream);
+
+/*
+ * Device: unpack int32-packed `wbits` codes along dim 0,
+ *   out[r, c] = (packed[r / (32/wbits), c] >> (wbits * (r % (32/wbits)))) & mask
+ * for r < num_rows; out is int32 [num_rows, cols]. Replaces
+ * quant_utils._unpack_rows (quant_utils.py:12-28). wbits in {2, 4, 8}.
+ */
+int oc_unpack_rows(const int32_t *packed, int32_t packed_rows, int32_t cols,
+                   int32_t wbits, int32_t num_rows, int32_t *out, void *stream);
+
+/*
+ * Device, test/inspection only: dequantize a GPTQ layer to out [N, K]
+ * (row n = output feature), bit-exact with quant_utils.dequant_gptq_to_fp
+ * (quant_utils.py:50-69):
+ *   out[n, k] = RNE_out( f32(scales[g(k), n]) * f32(code(k, n) - zero(g(k), n)) )
+ * g(k) = g_idx[k] (int32, device) or k / groupsize when g_idx == NULL.
+ * wbits in {4, 8} (8-bit: 4 codes per word, mask 0xFF). scale_dtype in
+ * {F16, BF16, F32}; out_dtype in {F16, BF16, F32}.
+ */
+int oc_int4_dequant(const int32_t *qweight, const void *scales,
+                    int32_t scale_dtype, const int32_t *qzeros,
+                    int32_t zero_mode, const int32_t *g_idx, int32_t groupsize,
+                    int32_t wbits, int32_t K, int32_t N, void *out,
+                    int32_t out_dtype, void *stream);
+
+/*
+ * Device: fused int4 dequant + GEMM, C[M, N] = A' @ Wd + bias, where
+ *   A'[m, k'] = kmap ? (kmap[k'] >= 0 ? A[m, kmap[k']] : 0) : A[m, k'],
+ *   Wd[k', n] = RNE_a( f32(scales[k'/group_rows, n]) * (code(k', n) - zero) )
+ * computed with fp32 accumulation and rounded once to a_dtype on store
+ * (bias added in fp32). Replaces the Triton launches of
+ * layers/fused_int4_linear.py:1194-1208 (FusedInt4Linear.forward), :504-532
+ * (fused_int4_gemm) and :904-919 (FusedInt4LinearPaddedGroups.forward), and
+ * the act-order packed path layers/packed_gptq_linear.py:66-74.
+ *   a        [M, K_logical] (row stride lda elements), a_dtype in {F16, BF16}
+ *   qweight  [K_phys/8, N] int32 (physical rows, see oc_int4_plan_groups)
+ *   scales   [K_phys/group_rows, N], scale_dtype in {F16, BF16}
+ *   qzeros   [K_phys/group_rows, N/8] int32
+ *   kmap     NULL or int32 [K_phys] (device)
+ *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
+ *   c        [M, N] (row stride ldc elements) of a_dtype
+ * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
+ * K_phys % group_rows == 0; without kmap K_logical == K_phys.
+ * The workspace (>= oc_int4_gemm_workspace_bytes) must be zero-filled
+ * before its first use; the library leaves it zero-filled after every call,
+ * so one workspace serves any sequence of calls on one stream. Calls that
+ * overlap in time must not share a workspace.
+ */
+int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
+                 int32_t K_logical, const int32_t *qweight, const void *scales,
+                 int32_t scale_dtype, const int32_t *qzeros, int32_t zero_mode,
+                 int32_t N, int32_t K_phys, int32_t group_rows,
+                 const int32_t *kmap, const void *bias, int32_t bias_dtype,
+                 void *c, int64_t ldc, void *workspace, size_t workspace_bytes,
+                 int32_t regime, void *stream);
+
+/* Workspace bytes oc_int4_gemm needs for this shape (0 if none). */
+size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys,
+                                    int32_t regime);
+
+/*
+ * Device, test/inspection only: RTN uint8-nibble dequant, bit-exact with
+ * quant_utils.dequant_extra_u8_to_weight (quant_utils.py:72-103): every
+ * operation is rounded to out_dtype (RNE), as torch does for 16-bit math:
+ *   w = code; zq = RNE(zero); sq = RNE(scale); d = RNE(w - zq); out = RNE(d * sq)
+ * qweight_u8 [rows, row_bytes] with row_bytes >= ceil(K/2); scales/zeros
+ * [rows, G] with K % G == 0 (G == 1: per row). out [rows, K].
+ * scale_dtype in {F16, BF16, F32}; zero_dtype in {F16, BF16, F32, U8, I32}.
+ */
+int oc_rtn_dequant(const uint8_t *qweight_u8, int32_t rows, int32_t row_bytes,
+                   const void *scales, int32_t scale_dtype, const void *zeros,
+                   int32_t zero_dtype, int32_t G, int32_t K, void *out,
+                   int32_t out_dtype, void *stream);
+
+/*
+ * Device: fused RTN linear, C[M, N] = X @ Wrtn^T + bias, with Wrtn the
+ * per-op-rounded dequant above in x_dtype, fp32 accumulation, one rounding
+ * on store. Replaces PackedRTNLinear.forward (layers/packed_linear.py:53-56).
+ * x [M, K] (row stride ldx), x_dtype in {F16, BF16}; qweight_u8 [N, row_bytes];
+ * scales/zeros [N, G]; bias NULL or [N] (rounded to x_dtype first, like
+ * `bias.to(x.dtype)` at packed_linear.py:55); c [M, N] (row stride ldc).
+ */
+int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M,
+                  int32_t K, const uint8_t *qweight_u8, int32_t row_bytes,
+                  const void *scales, int32_t scale_dtype, const void *zeros,
+                  int32_t zero_dtype, int32_t G, int32_t N, const void *bias,
+                  int32_t bias_dtype, void *c, int64_t ldc, void *stream);
+
+/*
+ * Device: packed RTN embedding lookup, out[t, :] = dequant(row ids[t]) in
+ * out_dtype. Replaces PackedEmbedding.forward (layers/packed_linear.py:93-104);
+ * the reference's output dtype rule (scales' dtype, fp16 for non-float
+ * scales, :98) is applied by the caller through out_dtype. ids are int64;
+ * an id outside [0, V) yields a zero row and sets the device flag
+ * `bad_id_flag` (int32, may be NULL) to 1.
+ */
+int oc_rtn_embedding(const int64_t *ids, int64_t T, const uint8_t *qweight_u8,
+                     int64_t V, int32_t row_bytes, const void *scales,
+                     int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
+                     int32_t G, int32_t D, void *out, int32_t out_dtype,
+                     int32_t *bad_id_flag, void *stream);
+
+/*
+ * Device: MoE routing prologue (no reference counterpart: the reference has
+ * no grouped GEMM; its MoE path loops over experts, layers/dsv4_packed_linear.py:95-98).
+ * Stable counting sort of the T*topk (token, slot) pairs by expert id:
+ *   expert_offsets[E+1] (exclusive prefix of per-expert counts),
+ *   sorted_pairs[T*topk] = pair index p = t*topk + j, grouped by expert,
+ *   ascending p within an expert. Ids outside [0, E) are dropped (not
+ *   counted). topk_ids is int64 [T, topk]. Single workgroup; T*topk <= 65536,
+ *   E <= 1024.
+ */
+int oc_moe_route(const int64_t *topk_ids, int32_t T, int32_t topk, int32_t E,
+                 int32_t *expert_offsets, int32_t *sorted_pairs, void *stream);
+
+/*
+ * Device: grouped int4 GEMM over E experts (no reference counterpart; see
+ * oc_moe_route). For every routed pair p = t*topk + j of expert e:
+ *   Y[p, :] = X[t, :] @ Wd_e        (fp32 accumulation, rounded to x_dtype)
+ * x [T, K] (row stride ldx) in {F16, BF16}; per-expert GPTQ tensors stacked
+ * on a leading E axis: qweight [E, K/8, N], scales [E, K/group_rows, N],
+ * qzeros [E, K/group_rows, N/8]; y [T*topk, N] (row stride ldy).
+ * K % 32 == 0, group_rows % 32 == 0, N % 64 == 0.
+ */
+int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T,
+                     int32_t topk, int32_t K, const int32_t *qweight,
+                     const void *scales, int32_t scale_dtype,
+                     const int32_t *qzeros, int32_t zero_mode,
+                     int32_t group_rows, int32_t E, int32_t N,
+                     const int32_t *expert_offsets, const int32_t *sorted_pairs,
+                     void *y, int64_t ldy, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ONECOMP_HIP_H */

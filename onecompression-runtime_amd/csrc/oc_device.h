@@ -1,0 +1,189 @@
+// Device-side building blocks shared by every kernel of libonecomp_hip.so:
+// element-type helpers, the exact GPTQ dequant, the RTN per-op-rounded dequant
+// and the gfx950 MFMA wrappers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "oc_internal.h"
+
+namespace oc {
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short v8i16;
+typedef __attribute__((__vector_size__(8 * sizeof(_Float16)))) _Float16 v8f16;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float v4f32;
+typedef __attribute__((__vector_size__(2 * sizeof(float)))) float v2f32;
+typedef __attribute__((__vector_size__(2 * sizeof(_Float16)))) _Float16 v2f16;
+typedef __attribute__((__vector_size__(2 * sizeof(__bf16)))) __bf16 v2bf16;
+
+template <typename To, typename From>
+__device__ __forceinline__ To bitcast(const From &v) {
+  return __builtin_bit_cast(To, v);
+}
+
+// ---- scalar conversions (all round-to-nearest-even) ------------------------
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return bitcast<float>(static_cast<uint32_t>(b) << 16);
+}
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  return static_cast<float>(bitcast<_Float16>(h));
+}
+// Two floats -> packed pair (lo = a, hi = b), RNE (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint32_t pack2_bf16(float a, float b) {
+  v2f32 v = {a, b};
+  return bitcast<uint32_t>(__builtin_convertvector(v, v2bf16));
+}
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b) {
+  v2f32 v = {a, b};
+  return bitcast<uint32_t>(__builtin_convertvector(v, v2f16));
+}
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (DT == OC_DTYPE_BF16) return pack2_bf16(a, b);
+  else return pack2_f16(a, b);
+}
+// Round a float to the 16-bit type DT and return it widened back to float.
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (DT == OC_DTYPE_F32) {
+    return x;
+  } else if constexpr (DT == OC_DTYPE_BF16) {
+    return bf16_to_f32(static_cast<uint16_t>(pack2_bf16(x, 0.f)));
+  } else {
+    return static_cast<float>(static_cast<_Float16>(x));
+  }
+}
+template <int DT>
+__device__ __forceinline__ float load_as_f32(const void *p, int64_t i) {
+  if constexpr (DT == OC_DTYPE_BF16) return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+  else if constexpr (DT == OC_DTYPE_F16) return f16_to_f32(static_cast<const uint16_t *>(p)[i]);
+  else return static_cast<const float *>(p)[i];
+}
+// Runtime-typed scalar load (load-time / epilogue paths only).
+__device__ __forceinline__ float load_any_f32(const void *p, int64_t i, int dt) {
+  switch (dt) {
+    case OC_DTYPE_BF16: return bf16_to_f32(static_cast<const uint16_t *>(p)[i]);
+    case OC_DTYPE_F16: return f16_to_f32(static_cast<const uint16_t *>(p)[i]);
+    case OC_DTYPE_F32: return static_cast<const float *>(p)[i];
+    case OC_DTYPE_U8: return static_cast<float>(static_cast<const uint8_t *>(p)[i]);
+    case OC_DTYPE_I32: return static_cast<float>(static_cast<const int32_t *>(p)[i]);
+    default: return 0.f;
+  }
+}
+
+// ---- GPTQ dequant ------------------------------------------------------------
+//
+// The reference dequant (quant_utils.py:68-69) is one exact fp32 product
+// s * (w - z) followed by a single rounding to the output type: with s a
+// 16-bit float (<= 11 significant bits) and |w - z| <= 15 the product has at
+// most 15 significant bits, so fp32 holds it exactly.
+//
+// Here each 4-bit code w is turned into the fp16 number 1024 + w by OR-ing it
+// into the mantissa of 0x6400 (= 1024.0h). For a column with scale s and zero
+// z, let c = -s * (1024 + z): both s * (1024 + w) and c need at most 22
+// significant bits, so they are exact in fp32, and the fused multiply-add
+// fma(1024 + w, s, c) (v_fma_mix_f32: the fp16 operand is read directly)
+// produces the exact s * (w - z). One VALU op per weight, plus a shared
+// shift/insert per code pair and one pack per output pair.
+
+struct GroupParam {
+  float s;  // scale as fp32 (exact)
+  float c;  // -s * (1024 + zero) (exact)
+};
+
+__device__ __forceinline__ GroupParam make_group_param(float s, int zero) {
+  GroupParam p;
+  p.s = s;
+  p.c = -s * static_cast<float>(1024 + zero);
+  return p;
+}
+
+// 4-bit codes at bit positions (4j, 4j+16) -> fp16 pair (1024 + code_j, 1024 + code_{j+4}).
+__device__ __forceinline__ uint32_t magic_pair(uint32_t q_shifted) {
+  return (q_shifted & 0x000F000Fu) | 0x64006400u;
+}
+
+// Dequantize the 8 codes of one packed word (code i at bits 4i) with one
+// group parameter; returns 4 dwords holding the 8 results in natural order
+// (dword d = codes 2d, 2d+1), each rounded once (RNE) to DT.
+template <int DT>
+__device__ __forceinline__ uint4 dequant8(uint32_t q, GroupParam gp) {
+  const v2f16 h0 = bitcast<v2f16>(magic_pair(q));        // codes 0,4
+  const v2f16 h1 = bitcast<v2f16>(magic_pair(q >> 4));   // codes 1,5
+  const v2f16 h2 = bitcast<v2f16>(magic_pair(q >> 8));   // codes 2,6
+  const v2f16 h3 = bitcast<v2f16>(magic_pair(q >> 12));  // codes 3,7
+  const float f0 = __builtin_fmaf(static_cast<float>(h0[0]), gp.s, gp.c);
+  const float f4 = __builtin_fmaf(static_cast<float>(h0[1]), gp.s, gp.c);
+  const float f1 = __builtin_fmaf(static_cast<float>(h1[0]), gp.s, gp.c);
+  const float f5 = __builtin_fmaf(static_cast<float>(h1[1]), gp.s, gp.c);
+  const float f2 = __builtin_fmaf(static_cast<float>(h2[0]), gp.s, gp.c);
+  const float f6 = __builtin_fmaf(static_cast<float>(h2[1]), gp.s, gp.c);
+  const float f3 = __builtin_fmaf(static_cast<float>(h3[0]), gp.s, gp.c);
+  const float f7 = __builtin_fmaf(static_cast<float>(h3[1]), gp.s, gp.c);
+  uint4 r;
+  r.x = pack2<DT>(f0, f1);
+  r.y = pack2<DT>(f2, f3);
+  r.z = pack2<DT>(f4, f5);
+  r.w = pack2<DT>(f6, f7);
+  return r;
+}
+
+// Zero point of column n from a packed qzeros row, with the v1/v2 convention.
+__device__ __forceinline__ int unpack_zero(uint32_t zword, int n, int zero_mode) {
+  const int zst = static_cast<int>((zword >> (4 * (n & 7))) & 0xFu);
+  return zero_mode == OC_ZERO_V1 ? ((zst + 1) & 0xF) : zst;
+}
+
+// ---- RTN dequant (per-op rounding) --------------------------------------------
+//
+// quant_utils.py:91-103 evaluates (w - z) * s in the compute dtype, each torch
+// op rounding its result. Each op is emulated as an fp32 op followed by one
+// RNE to DT; for + - * on p-bit operands an intermediate of >= 2p+2 bits makes
+// this double rounding harmless (fp32: 24 >= 18 for bf16, 24 >= 24 for fp16).
+struct RtnParam {
+  float zq;  // RNE_DT(zero)
+  float sq;  // RNE_DT(scale)
+};
+
+template <int DT>
+__device__ __forceinline__ float rtn_value(int code, RtnParam p) {
+  const float d = round_to<DT>(static_cast<float>(code) - p.zq);
+  return round_to<DT>(d * p.sq);
+}
+
+template <int DT>
+__device__ __forceinline__ uint4 rtn_dequant8(uint32_t q, RtnParam p) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) f[i] = rtn_value<DT>(static_cast<int>((q >> (4 * i)) & 0xFu), p);
+  uint4 r;
+  r.x = pack2<DT>(f[0], f[1]);
+  r.y = pack2<DT>(f[2], f[3]);
+  r.z = pack2<DT>(f[4], f[5]);
+  r.w = pack2<DT>(f[6], f[7]);
+  return r;
+}
+
+// ---- MFMA -----------------------------------------------------------------------
+//
+// v_mfma_f32_16x16x32_{bf16,f16} operand layout (one wave, lane l):
+//   A[16 x 32]: lane l holds row (l % 16), k = 8*(l / 16) + 0..7
+//   B[32 x 16]: lane l holds col (l % 16), k = 8*(l / 16) + 0..7
+//   D[16 x 16]: lane l holds col (l % 16), rows 4*(l / 16) + 0..3
+template <int DT>
+__device__ __forceinline__ v4f32 mfma16x16x32(uint4 a, uint4 b, v4f32 acc) {
+  if constexpr (DT == OC_DTYPE_BF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(bitcast<v8i16>(a), bitcast<v8i16>(b), acc, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<v8f16>(a), bitcast<v8f16>(b), acc, 0, 0, 0);
+  }
+}
+
+// Agent-scope relaxed load that bypasses the (non-coherent) per-CU L1.
+__device__ __forceinline__ float load_coherent(const float *p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace oc

@@ -1,0 +1,47 @@
+// Host-side helpers shared by the library's translation units: the public
+// ABI, status reporting and launch-argument checks.
+#pragma once
+
+#include <stdarg.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "onecomp_hip.h"
+
+namespace oc {
+
+// Records a formatted error message for oc_last_error() and returns `status`.
+int fail(int status, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+
+// Clears the thread's last error.
+void clear_error();
+
+inline bool is_half_dtype(int dt) { return dt == OC_DTYPE_F16 || dt == OC_DTYPE_BF16; }
+inline bool is_float_dtype(int dt) { return is_half_dtype(dt) || dt == OC_DTYPE_F32; }
+inline size_t dtype_bytes(int dt) {
+  switch (dt) {
+    case OC_DTYPE_F16:
+    case OC_DTYPE_BF16: return 2;
+    case OC_DTYPE_F32:
+    case OC_DTYPE_I32: return 4;
+    case OC_DTYPE_U8: return 1;
+    default: return 0;
+  }
+}
+inline bool aligned(const void *p, size_t bytes) {
+  return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
+}
+
+}  // namespace oc
+
+// Returns OC_ERR_HIP (with the HIP error string) from the enclosing function
+// when a HIP call fails.
+#define OC_HIP_RETURN_IF_ERROR(expr)                                                   \
+  do {                                                                                 \
+    hipError_t oc_err_ = (expr);                                                       \
+    if (oc_err_ != hipSuccess)                                                         \
+      return ::oc::fail(OC_ERR_HIP, "%s failed: %s", #expr, hipGetErrorString(oc_err_)); \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+#define OC_RETURN_LAUNCH_STATUS() OC_HIP_RETURN_IF_ERROR(hipGetLastError())

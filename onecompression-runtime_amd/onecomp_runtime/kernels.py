@@ -1,0 +1,234 @@
+"""Functional wrappers over the HIP C ABI (one function per entry point).
+
+Each wrapper validates what the ABI cannot see (dtypes, devices, contiguity),
+allocates outputs with ``torch.empty`` on the inputs' device, and launches on
+torch's current stream. Nothing here computes on the host except
+:func:`plan_groups`, the load-time row-layout planner.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _hip
+from ._hip import check, dtype_code, lib, ptr, require_device, stream_of
+
+
+@dataclass(frozen=True)
+class GroupPlan:
+    """Physical row layout of a GPTQ layer (see ``oc_int4_plan_groups``)."""
+
+    k_phys: int
+    group_rows: int
+    num_groups: int
+    identity: bool
+    kmap: np.ndarray  # int32 [k_phys]; -1 marks a zero row
+
+
+def plan_groups(in_features: int, groupsize: int, g_idx: torch.Tensor | None = None) -> GroupPlan:
+    """Host-side planner: uniform physical groups of a multiple of 32 rows.
+
+    Handles act-order ``g_idx`` (rows sorted by group), odd group sizes (each
+    group padded to 32 rows, like the reference's ``_repack_groups_to_32``,
+    layers/fused_int4_linear.py:94-124) and K padding.
+    """
+    K = int(in_features)
+    gi = None
+    if g_idx is not None:
+        gi = np.ascontiguousarray(g_idx.detach().to("cpu", torch.int64).numpy())
+        if gi.shape != (K,):
+            raise ValueError(f"g_idx must have shape ({K},), got {tuple(gi.shape)}")
+    k_phys, rows, ngroups, ident = (ctypes.c_int32() for _ in range(4))
+    gptr = gi.ctypes.data if gi is not None else None
+    check(
+        lib().oc_int4_plan_groups(gptr, K, int(groupsize), None, 0, ctypes.byref(k_phys),
+                                  ctypes.byref(rows), ctypes.byref(ngroups), ctypes.byref(ident)),
+        "oc_int4_plan_groups",
+    )
+    kmap = np.empty(k_phys.value, dtype=np.int32)
+    check(
+        lib().oc_int4_plan_groups(gptr, K, int(groupsize), kmap.ctypes.data, kmap.size,
+                                  ctypes.byref(k_phys), ctypes.byref(rows), ctypes.byref(ngroups),
+                                  ctypes.byref(ident)),
+        "oc_int4_plan_groups",
+    )
+    return GroupPlan(k_phys.value, rows.value, ngroups.value, bool(ident.value), kmap)
+
+
+def repack_rows(qweight: torch.Tensor, in_features: int, kmap: torch.Tensor | None,
+                k_phys: int) -> torch.Tensor:
+    """Re-lay packed int4 rows on the device: row k' <- input row kmap[k']."""
+    dev = require_device(qweight, kmap)
+    if qweight.dtype != torch.int32:
+        raise ValueError("qweight must be int32")
+    qweight = qweight.contiguous()
+    N = qweight.shape[1]
+    out = torch.empty((k_phys // 8, N), dtype=torch.int32, device=dev)
+    check(
+        lib().oc_int4_repack_rows(ptr(qweight), int(in_features), N, ptr(kmap), int(k_phys), ptr(out),
+                                  stream_of(dev)),
+        "oc_int4_repack_rows",
+    )
+    return out
+
+
+def unpack_rows(packed: torch.Tensor, num_rows: int, wbits: int) -> torch.Tensor:
+    """int32 [R, C] of packed codes -> int32 [num_rows, C] (quant_utils.py:12-28)."""
+    if 32 % wbits != 0:
+        raise ValueError(f"wbits must divide 32, got {wbits}")
+    dev = require_device(packed)
+    packed = packed.contiguous()
+    if packed.dtype != torch.int32:
+        raise ValueError("packed must be int32")
+    R, C = packed.shape
+    out = torch.empty((num_rows, C), dtype=torch.int32, device=dev)
+    check(lib().oc_unpack_rows(ptr(packed), R, C, int(wbits), int(num_rows), ptr(out), stream_of(dev)),
+          "oc_unpack_rows")
+    return out
+
+
+def int4_dequant(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor,
+                 g_idx: torch.Tensor | None, in_features: int, out_features: int,
+                 dtype: torch.dtype, v1: bool = True, wbits: int = 4,
+                 groupsize: int | None = None) -> torch.Tensor:
+    """Dense [out, in] weight, bit-exact with quant_utils.dequant_gptq_to_fp."""
+    dev = require_device(qweight, scales, qzeros, g_idx)
+    K, N = int(in_features), int(out_features)
+    gi32 = None
+    if g_idx is not None:
+        gi32 = g_idx.to(device=dev, dtype=torch.int32).contiguous()
+    elif groupsize is None:
+        raise ValueError("either g_idx or groupsize is required")
+    qweight, scales, qzeros = qweight.contiguous(), scales.contiguous(), qzeros.contiguous()
+    out = torch.empty((N, K), dtype=dtype, device=dev)
+    check(
+        lib().oc_int4_dequant(ptr(qweight), ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
+                              _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, ptr(gi32),
+                              int(groupsize or 0), int(wbits), K, N, ptr(out), dtype_code(dtype),
+                              stream_of(dev)),
+        "oc_int4_dequant",
+    )
+    return out
+
+
+def int4_gemm(a_2d: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor,
+              *, in_features: int, k_phys: int, group_rows: int, v1: bool,
+              kmap: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+              out: torch.Tensor | None = None, regime: int = _hip.OC_REGIME_AUTO) -> torch.Tensor:
+    """C[M, N] = A @ dequant(W) + bias on the HIP device (fp32 accumulation)."""
+    dev = require_device(a_2d, qweight, scales, qzeros, kmap, bias)
+    if a_2d.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"activations must be fp16 or bf16, got {a_2d.dtype}")
+    if a_2d.stride(-1) != 1:
+        a_2d = a_2d.contiguous()
+    M = a_2d.shape[0]
+    N = qweight.shape[1]
+    if out is None:
+        out = torch.empty((M, N), dtype=a_2d.dtype, device=dev)
+    ws, nbytes = _hip.gemm_workspace(dev, M, N, k_phys, regime)
+    check(
+        lib().oc_int4_gemm(
+            ptr(a_2d), a_2d.stride(0), dtype_code(a_2d.dtype), M, int(in_features), ptr(qweight),
+            ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
+            _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, N, int(k_phys), int(group_rows), ptr(kmap),
+            ptr(bias), dtype_code(bias.dtype) if bias is not None else 0, ptr(out), out.stride(0),
+            ptr(ws), nbytes, int(regime), stream_of(dev),
+        ),
+        "oc_int4_gemm",
+    )
+    return out
+
+
+def rtn_dequant(qweight_u8: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+                in_features: int, out_features: int, dtype: torch.dtype) -> torch.Tensor:
+    """Dense [rows, in] weight, bit-exact with quant_utils.dequant_extra_u8_to_weight."""
+    dev = require_device(qweight_u8, scales, zeros)
+    qweight_u8, scales, zeros = qweight_u8.contiguous(), scales.contiguous(), zeros.contiguous()
+    rows = int(out_features)
+    K = int(in_features)
+    G = scales.shape[1]
+    out = torch.empty((rows, K), dtype=dtype, device=dev)
+    check(
+        lib().oc_rtn_dequant(ptr(qweight_u8), rows, qweight_u8.shape[1], ptr(scales),
+                             dtype_code(scales.dtype), ptr(zeros), dtype_code(zeros.dtype), G, K,
+                             ptr(out), dtype_code(dtype), stream_of(dev)),
+        "oc_rtn_dequant",
+    )
+    return out
+
+
+def rtn_linear(x_2d: torch.Tensor, qweight_u8: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
+               in_features: int, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused PackedRTNLinear forward for fp16/bf16 activations."""
+    dev = require_device(x_2d, qweight_u8, scales, zeros, bias)
+    if x_2d.stride(-1) != 1:
+        x_2d = x_2d.contiguous()
+    M = x_2d.shape[0]
+    N = qweight_u8.shape[0]
+    G = scales.shape[1]
+    c = torch.empty((M, N), dtype=x_2d.dtype, device=dev)
+    check(
+        lib().oc_rtn_linear(ptr(x_2d), x_2d.stride(0), dtype_code(x_2d.dtype), M, int(in_features),
+                            ptr(qweight_u8), qweight_u8.shape[1], ptr(scales), dtype_code(scales.dtype),
+                            ptr(zeros), dtype_code(zeros.dtype), G, N, ptr(bias),
+                            dtype_code(bias.dtype) if bias is not None else 0, ptr(c), c.stride(0),
+                            stream_of(dev)),
+        "oc_rtn_linear",
+    )
+    return c
+
+
+def rtn_embedding(ids: torch.Tensor, qweight_u8: torch.Tensor, scales: torch.Tensor,
+                  zeros: torch.Tensor, embedding_dim: int, dtype: torch.dtype,
+                  bad_id_flag: torch.Tensor | None = None) -> torch.Tensor:
+    """out[t, :] = RTN dequant of table row ids[t], shape [T, D]."""
+    dev = require_device(ids, qweight_u8, scales, zeros, bad_id_flag)
+    flat = ids.reshape(-1)
+    if flat.dtype != torch.int64:
+        flat = flat.long()
+    flat = flat.contiguous()
+    D = int(embedding_dim)
+    out = torch.empty((flat.shape[0], D), dtype=dtype, device=dev)
+    check(
+        lib().oc_rtn_embedding(ptr(flat), flat.shape[0], ptr(qweight_u8), qweight_u8.shape[0],
+                               qweight_u8.shape[1], ptr(scales), dtype_code(scales.dtype), ptr(zeros),
+                               dtype_code(zeros.dtype), scales.shape[1], D, ptr(out), dtype_code(dtype),
+                               ptr(bad_id_flag), stream_of(dev)),
+        "oc_rtn_embedding",
+    )
+    return out
+
+
+def moe_route(topk_ids: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Stable counting sort of routed (token, slot) pairs by expert."""
+    dev = require_device(topk_ids)
+    ids = topk_ids.to(torch.int64).contiguous()
+    T, topk = ids.shape
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    sorted_pairs = torch.empty(T * topk, dtype=torch.int32, device=dev)
+    check(lib().oc_moe_route(ptr(ids), T, topk, int(num_experts), ptr(offsets), ptr(sorted_pairs),
+                             stream_of(dev)), "oc_moe_route")
+    return offsets, sorted_pairs
+
+
+def int4_moe_gemm(x: torch.Tensor, topk: int, qweight: torch.Tensor, scales: torch.Tensor,
+                  qzeros: torch.Tensor, expert_offsets: torch.Tensor, sorted_pairs: torch.Tensor,
+                  *, group_rows: int = 32, v1: bool = True) -> torch.Tensor:
+    """Y[t*topk + j, :] = x[t] @ dequant(W_{e(t,j)}) for every routed pair."""
+    dev = require_device(x, qweight, scales, qzeros, expert_offsets, sorted_pairs)
+    x, qweight, scales, qzeros = x.contiguous(), qweight.contiguous(), scales.contiguous(), qzeros.contiguous()
+    T, K = x.shape
+    E, _, N = qweight.shape
+    y = torch.empty((T * topk, N), dtype=x.dtype, device=dev)
+    check(
+        lib().oc_int4_moe_gemm(ptr(x), x.stride(0), dtype_code(x.dtype), T, int(topk), K,
+                               ptr(qweight), ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
+                               _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, int(group_rows), E, N,
+                               ptr(expert_offsets), ptr(sorted_pairs), ptr(y), y.stride(0),
+                               stream_of(dev)),
+        "oc_int4_moe_gemm",
+    )
+    return y

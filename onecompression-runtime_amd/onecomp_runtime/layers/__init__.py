@@ -1,0 +1,34 @@
+"""Int4 inference layers executed by the HIP library (gfx950).
+
+- :class:`FusedInt4Linear` / :func:`fused_int4_gemm` - GPTQ groupsize-32 int4
+  Linear (v1 or v2 zeros), fused dequant + GEMM.
+- :class:`FusedInt4LinearPaddedGroups` - odd groupsizes re-laid into 32-row groups.
+- :class:`FusedInt4LinearAnyGroup` - any groupsize.
+- :class:`PackedGPTQLinear` - any groupsize, act-order ``g_idx``, 4/8-bit.
+- :class:`PackedRTNLinear` / :class:`PackedEmbedding` - RTN uint8-nibble layers.
+- :class:`GemLiteInt4Linear` / :func:`gemlite_available` - import-compatible
+  names only (GemLite is never available on this build).
+"""
+from __future__ import annotations
+
+from .fused_int4_linear import (
+    FusedInt4Linear,
+    FusedInt4LinearAnyGroup,
+    FusedInt4LinearPaddedGroups,
+    fused_int4_gemm,
+)
+from .gemlite_int4_linear import GemLiteInt4Linear, gemlite_available
+from .packed_gptq_linear import PackedGPTQLinear
+from .packed_linear import PackedEmbedding, PackedRTNLinear
+
+__all__ = [
+    "FusedInt4Linear",
+    "FusedInt4LinearAnyGroup",
+    "FusedInt4LinearPaddedGroups",
+    "fused_int4_gemm",
+    "GemLiteInt4Linear",
+    "gemlite_available",
+    "PackedGPTQLinear",
+    "PackedRTNLinear",
+    "PackedEmbedding",
+]

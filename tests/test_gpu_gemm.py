@@ -1,0 +1,256 @@
+"""Parity of the fused int4 GEMM (both regimes) with the oracle's CPU
+packed/eager path, on the benchmark workloads and on edge cases.
+
+Tolerance (GEMM outputs, floating point): max|out - ref| <= 2e-2 * max|ref|
+and cosine >= 0.9999, ref = dequant (bit-exact) + fp32-accumulated linear.
+The in-GEMM dequant itself is checked bit-exactly with one-hot activations:
+row m of A = e_k gives C[m, :] = Wd[:, k] exactly.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_helpers import assert_gemm_close, bits16, layer_oracle_inputs, np32, oracle_bits, say
+from oracle import onecomp_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+SPLITK, TILED, AUTO = 1, 2, 0
+
+
+def _module_for(layer, dtype=torch.bfloat16):
+    """The layer the hip backend builds for this synthetic layer."""
+    from onecomp_runtime import backend
+
+    entry = dict(in_features=layer.K, out_features=layer.N, wbits=4, groupsize=layer.groupsize,
+                 actorder=layer.g_idx is not None,
+                 checkpoint_format="gptq" if layer.v1 else "gptq_v2", name="l")
+    st = dict(qweight=layer.qweight, scales=layer.scales, qzeros=layer.qzeros)
+    if layer.g_idx is not None:
+        st["g_idx"] = layer.g_idx
+    mod, kind = backend.build_quant_layer(entry, st, "hip", dtype, torch.device(DEV))
+    assert kind == "hip"
+    return mod
+
+
+def _oracle_out(layer, x: torch.Tensor, dtype="bf16", bias=None):
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    return O.gptq_linear(np32(x), qw, sc, qz, g_idx, layer.K, layer.N, dtype, layer.v1,
+                         bias=None if bias is None else np32(bias))
+
+
+def _gemm_raw(mod, x, regime):
+    from onecomp_runtime import kernels
+
+    return kernels.int4_gemm(x, mod.qweight, mod.scales, mod.qzeros, in_features=mod.in_features,
+                             k_phys=mod.k_phys, group_rows=mod.group_rows, v1=mod.v1, kmap=mod.kmap,
+                             bias=mod.bias, regime=regime)
+
+
+# -- benchmark workloads ------------------------------------------------------
+def test_gptq_gs32_m16():
+    from onecomp_runtime import synthetic
+
+    say("gptq_gs32_m16 M=16 K=N=4096")
+    layer = synthetic.gptq_layer(4096, 4096, seed=20260)
+    x = synthetic.activations(16, 4096, seed=20261)
+    mod = _module_for(layer)
+    assert type(mod).__name__ == "FusedInt4Linear"
+    out = mod(x.to(DEV))
+    assert out.dtype == torch.bfloat16 and out.shape == (16, 4096)
+    assert_gemm_close(out, _oracle_out(layer, x), "gptq_gs32_m16")
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 17408), (17408, 5120), (5120, 1024)])
+@pytest.mark.parametrize("M", [1, 8])
+def test_decode_actorder(K, N, M):
+    from onecomp_runtime import synthetic
+
+    say(f"decode_actorder M={M} K={K} N={N}")
+    layer = synthetic.gptq_layer(K, N, seed=20270 + K + N, act_order=True)
+    x = synthetic.activations(M, K, seed=20271 + M)
+    mod = _module_for(layer)
+    assert type(mod).__name__ == "PackedGPTQLinear" and mod.kmap is not None
+    assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), f"decode M={M} K={K} N={N}")
+
+
+@pytest.mark.parametrize("K,N", [(3072, 3072), (3072, 12288), (12288, 3072)])
+def test_dit_large_m_v2(K, N):
+    from onecomp_runtime import synthetic
+
+    say(f"dit_large_m M=4096 K={K} N={N} (v2)")
+    layer = synthetic.gptq_layer(K, N, seed=20280 + K + N, v1=False)
+    x = synthetic.activations(4096, K, seed=20281, outliers=True)
+    mod = _module_for(layer)
+    out = mod(x.to(DEV))
+    rows = slice(0, 4096) if K * N <= 3072 * 3072 else slice(0, 512)
+    assert_gemm_close(out[rows], _oracle_out(layer, x[rows]), f"dit K={K} N={N}")
+
+
+def test_padded_gs26():
+    from onecomp_runtime import synthetic
+
+    say("padded_gs26 M=256 K=1040 N=3072")
+    layer = synthetic.gptq_layer(1040, 3072, seed=20290, groupsize=26, pad_rows_to=1056)
+    x = synthetic.activations(256, 1040, seed=20291)
+    mod = _module_for(layer)
+    assert type(mod).__name__ == "FusedInt4LinearPaddedGroups"
+    assert mod.padded_in_features == 1280
+    assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), "padded gs26")
+
+
+# -- bit-exact in-GEMM dequant via one-hot activations ------------------------
+@pytest.mark.parametrize("regime", [SPLITK, TILED])
+@pytest.mark.parametrize("kind", ["gs32_v1", "v2", "actorder", "gs26", "gs128", "fp16"])
+def test_gemm_dequant_bit_exact_one_hot(regime, kind):
+    from onecomp_runtime import synthetic
+
+    K, N = 1024, 192
+    kw = dict(seed=31)
+    dtype = torch.float16 if kind == "fp16" else torch.bfloat16
+    if kind == "v2":
+        kw["v1"] = False
+    if kind == "actorder":
+        kw["act_order"] = True
+    if kind == "gs26":
+        K, kw["groupsize"] = 1040, 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer, dtype)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16" if dtype == torch.bfloat16 else "f16", layer.v1)
+    rng = np.random.default_rng(0)
+    ks = rng.choice(K, 48, replace=False)
+    x = torch.zeros((48, K), dtype=dtype)
+    x[torch.arange(48), torch.from_numpy(ks)] = 1.0
+    say(f"one-hot dequant kind={kind} regime={regime}")
+    out = _gemm_raw(mod, x.to(DEV), regime)
+    assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
+
+
+# -- regimes and shapes -------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 3, 16, 17, 33, 64])
+def test_splitk_and_tiled_agree_with_oracle(M):
+    from onecomp_runtime import synthetic
+
+    K, N = 2048, 640
+    layer = synthetic.gptq_layer(K, N, seed=40 + M)
+    x = synthetic.activations(M, K, seed=41)
+    mod = _module_for(layer)
+    ref = _oracle_out(layer, x)
+    for regime in (SPLITK, TILED):
+        say(f"regime={regime} M={M}")
+        assert_gemm_close(_gemm_raw(mod, x.to(DEV), regime), ref, f"regime {regime} M={M}")
+
+
+@pytest.mark.parametrize("M,K,N", [(65, 256, 8), (100, 1000, 24), (257, 512, 200), (300, 96, 64),
+                                   (1, 32, 8), (2, 4096, 136)])
+def test_ragged_shapes(M, K, N):
+    from onecomp_runtime import synthetic
+
+    say(f"ragged M={M} K={K} N={N}")
+    layer = synthetic.gptq_layer(K, N, seed=50)
+    x = synthetic.activations(M, K, seed=51)
+    mod = _module_for(layer)
+    assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), f"ragged {M}x{K}x{N}")
+
+
+def test_empty_batch():
+    from onecomp_runtime import synthetic
+
+    layer = synthetic.gptq_layer(256, 64, seed=52)
+    mod = _module_for(layer)
+    say("empty batch")
+    out = mod(torch.zeros((0, 256), dtype=torch.bfloat16, device=DEV))
+    assert out.shape == (0, 64)
+    out3 = mod(torch.zeros((2, 0, 256), dtype=torch.bfloat16, device=DEV))
+    assert out3.shape == (2, 0, 64)
+
+
+@pytest.mark.parametrize("bias_dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("M", [4, 300])
+def test_bias(bias_dtype, M):
+    from onecomp_runtime import synthetic
+    from onecomp_runtime.layers import FusedInt4Linear
+
+    K, N = 512, 256
+    layer = synthetic.gptq_layer(K, N, seed=53)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(1)).to(bias_dtype)
+    mod = FusedInt4Linear(K, N, layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV),
+                          bias=bias.to(DEV))
+    x = synthetic.activations(M, K, seed=54)
+    say(f"bias {bias_dtype} M={M}")
+    ref = _oracle_out(layer, x, bias=bias.float())
+    assert_gemm_close(mod(x.to(DEV)), ref, "bias")
+
+
+def test_fp16_and_fp32_activations():
+    from onecomp_runtime import synthetic
+    from onecomp_runtime.layers import FusedInt4Linear
+
+    K, N = 1024, 512
+    layer = synthetic.gptq_layer(K, N, seed=55)
+    mod = FusedInt4Linear(K, N, layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV))
+    x = synthetic.activations(24, K, seed=56, dtype=torch.float16)
+    say("fp16 activations")
+    assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x, "f16"), "fp16")
+    say("fp32 activations")
+    out32 = mod(x.float().to(DEV))
+    assert out32.dtype == torch.float32  # computed in fp16, returned as fp32
+    assert_gemm_close(out32, _oracle_out(layer, x, "f16"), "fp32")
+
+
+def test_3d_and_noncontiguous_input():
+    from onecomp_runtime import synthetic
+
+    K, N = 512, 128
+    layer = synthetic.gptq_layer(K, N, seed=57)
+    mod = _module_for(layer)
+    x = synthetic.activations(2 * 5, K, seed=58)
+    say("3-D input")
+    out = mod(x.reshape(2, 5, K).to(DEV))
+    assert out.shape == (2, 5, N)
+    assert_gemm_close(out.reshape(10, N), _oracle_out(layer, x), "3d")
+    wide = torch.zeros((10, 2 * K), dtype=torch.bfloat16)
+    wide[:, ::2] = x
+    say("strided input")
+    assert_gemm_close(mod(wide.to(DEV)[:, ::2]), _oracle_out(layer, x), "strided")
+
+
+@pytest.mark.parametrize("regime", [SPLITK, TILED])
+def test_deterministic_and_workspace_self_cleaning(regime):
+    from onecomp_runtime import _hip, synthetic
+
+    K, N, M = 8192, 1024, 8 if regime == SPLITK else 128
+    layer = synthetic.gptq_layer(K, N, seed=59)
+    mod = _module_for(layer)
+    x = synthetic.activations(M, K, seed=60).to(DEV)
+    say(f"determinism regime={regime}")
+    a = _gemm_raw(mod, x, regime)
+    b = _gemm_raw(mod, x, regime)
+    assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    nbytes = int(_hip.lib().oc_int4_gemm_workspace_bytes(M, N, mod.k_phys, regime))
+    if nbytes:
+        ws = _hip.workspace.get(x.device, nbytes)
+        tiles = 16  # at least this many tile counters sit at the front of the workspace
+        assert int(ws[: 4 * tiles].view(torch.int32).abs().sum().item()) == 0
+
+
+def test_abi_rejects_bad_arguments():
+    from onecomp_runtime import kernels, synthetic
+
+    layer = synthetic.gptq_layer(256, 64, seed=61)
+    qw, sc, qz = layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV)
+    x = synthetic.activations(4, 256, seed=62).to(DEV)
+    say("ABI argument errors")
+    with pytest.raises(ValueError):  # K_phys not a multiple of 32
+        kernels.int4_gemm(x, qw, sc, qz, in_features=256, k_phys=250, group_rows=32, v1=True)
+    with pytest.raises(ValueError):  # N not a multiple of 8
+        kernels.int4_gemm(x, qw[:, :60], sc[:, :60], qz, in_features=256, k_phys=256, group_rows=32,
+                          v1=True)
+    with pytest.raises(NotImplementedError):  # split-K regime is for M <= 64
+        kernels.int4_gemm(torch.zeros((65, 256), dtype=torch.bfloat16, device=DEV), qw, sc, qz,
+                          in_features=256, k_phys=256, group_rows=32, v1=True, regime=SPLITK)
+    with pytest.raises(RuntimeError):  # host tensors are refused
+        kernels.int4_gemm(x.cpu(), qw, sc, qz, in_features=256, k_phys=256, group_rows=32, v1=True)

@@ -1,0 +1,170 @@
+"""Host-side checks that need no GPU: the C ABI library loads and exports
+every declared symbol, the host-only layout planner, backend routing and
+argument errors, and the synthetic data packers."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import onecomp_oracle as O
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "onecomp_hip.h"
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(oc_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_symbol():
+    from onecomp_runtime import _hip
+
+    names = _declared_functions()
+    assert len(names) >= 12
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) == set(_hip.SIGNATURES), set(names) ^ set(_hip.SIGNATURES)
+
+
+def test_status_strings_and_version():
+    from onecomp_runtime import _hip
+
+    lib = _hip.lib()
+    assert lib.oc_status_string(0) == b"OC_OK"
+    assert lib.oc_status_string(_hip.OC_ERR_SHAPE) == b"OC_ERR_SHAPE"
+    assert lib.oc_version() >= 100
+
+
+def test_error_mapping_and_last_error():
+    from onecomp_runtime import _hip, kernels
+
+    with pytest.raises(ValueError, match="K must be positive"):
+        kernels.plan_groups(0, 32)
+    assert "K must be positive" in _hip.last_error()
+    with pytest.raises(NotImplementedError):
+        _hip.check(_hip.OC_ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _hip.check(_hip.OC_ERR_HIP, "x")
+
+
+@pytest.mark.parametrize("K,gs", [(4096, 32), (5120, 128), (1040, 26), (1000, 32), (96, 13), (64, 64)])
+def test_plan_groups_default_grouping(K, gs):
+    from onecomp_runtime import kernels
+
+    p = kernels.plan_groups(K, gs)
+    G = -(-K // gs)
+    assert p.num_groups == G
+    assert p.group_rows % 32 == 0 and p.group_rows >= min(gs, K)
+    assert p.k_phys == G * p.group_rows
+    valid = p.kmap[p.kmap >= 0]
+    assert np.array_equal(np.sort(valid), np.arange(K))  # every column exactly once
+    rows = np.nonzero(p.kmap >= 0)[0]
+    assert np.array_equal(rows // p.group_rows, p.kmap[rows] // gs)  # row's group == column's group
+    assert p.identity == (gs % 32 == 0 and K % gs == 0) or (p.identity and K % 32 == 0)
+
+
+def test_plan_groups_act_order_sorts_by_group_stably():
+    from onecomp_runtime import kernels
+
+    rng = np.random.default_rng(0)
+    K, gs = 512, 32
+    g_idx = rng.permutation(K) // gs
+    p = kernels.plan_groups(K, gs, torch.from_numpy(g_idx))
+    assert p.k_phys == K and p.group_rows == 32 and not p.identity
+    assert np.array_equal(p.kmap, np.argsort(g_idx, kind="stable"))
+    # identity g_idx is recognised
+    p2 = kernels.plan_groups(K, gs, torch.arange(K) // gs)
+    assert p2.identity
+
+
+def test_plan_groups_rejects_bad_g_idx():
+    from onecomp_runtime import kernels
+
+    with pytest.raises(ValueError):
+        kernels.plan_groups(64, 32, torch.full((64,), -1))
+    with pytest.raises(ValueError):
+        kernels.plan_groups(64, 32, torch.zeros(10, dtype=torch.long))
+    with pytest.raises(NotImplementedError):  # one giant group among many tiny ones
+        g = torch.arange(4096) // 1
+        g[:4000] = 0
+        kernels.plan_groups(4096, 32, g)
+
+
+def test_synthetic_packers_agree_with_oracle():
+    from onecomp_runtime import synthetic
+
+    layer = synthetic.gptq_layer(72, 16, seed=1, groupsize=32, v1=True)
+    assert np.array_equal(layer.qweight.numpy(), O.pack_rows(layer.codes.numpy()))
+    assert np.array_equal(layer.qzeros.numpy(), O.pack_zeros(layer.zeros.numpy(), v1=True))
+    v2 = synthetic.gptq_layer(64, 16, seed=1, v1=False)
+    assert np.array_equal(v2.qzeros.numpy(), O.pack_zeros(v2.zeros.numpy(), v1=False))
+    padded = synthetic.gptq_layer(1040, 8, seed=2, groupsize=26, pad_rows_to=1056)
+    assert padded.qweight.shape == (132, 8) and (padded.qweight[130:] == 0).all()
+    rtn = synthetic.rtn_layer(4, 10, seed=3)
+    assert np.array_equal(O.rtn_unpack(rtn.qweight_u8.numpy(), 10), rtn.codes.numpy())
+
+
+def test_resolve_backend_and_dtype():
+    from onecomp_runtime import backend
+
+    assert backend.resolve_backend("auto") == "hip"
+    assert backend.resolve_backend(None) == "hip"
+    assert backend.resolve_backend("fused") == "fused"
+    assert backend.resolve_backend("auto", use_fused=False) == "eager"
+    with pytest.raises(ValueError):
+        backend.resolve_backend("tensorrt")
+    for b in ("gemlite", "a8w4", "nvfp4_ffn"):
+        with pytest.raises(RuntimeError):
+            backend.resolve_backend(b)
+    assert backend.resolve_dtype("bf16") is torch.bfloat16
+    with pytest.raises(ValueError):
+        backend.resolve_dtype("int8")
+
+
+def test_routing_predicates():
+    from onecomp_runtime import backend
+
+    base = dict(wbits=4, groupsize=32, in_features=4096, out_features=4096, actorder=False)
+    assert backend.can_use_fused(base)
+    assert not backend.can_use_fused({**base, "actorder": True})
+    assert backend.can_use_fused_padded_groups({**base, "groupsize": 26, "in_features": 1040})
+    assert not backend.can_use_fused_padded_groups(base)
+    assert backend.is_v1({}) and backend.is_v1({"checkpoint_format": "gptq"})
+    assert not backend.is_v1({"checkpoint_format": "gptq_v2"})
+
+
+def test_modules_refuse_host_tensors_without_fallback():
+    from onecomp_runtime.layers import FusedInt4Linear, FusedInt4LinearPaddedGroups
+
+    layer = O.pack_rows(np.zeros((64, 16), np.int64))
+    lin = FusedInt4Linear(64, 16, torch.from_numpy(layer), torch.ones(2, 16, dtype=torch.float16),
+                          torch.zeros(2, 2, dtype=torch.int32))
+    with pytest.raises(RuntimeError, match="HIP device"):
+        lin(torch.zeros(1, 64, dtype=torch.bfloat16))
+    with pytest.raises(AssertionError):
+        FusedInt4Linear(64, 16, torch.from_numpy(layer), torch.ones(1, 16, dtype=torch.float16),
+                        torch.zeros(1, 2, dtype=torch.int32), groupsize=64)
+    with pytest.raises(ValueError):
+        FusedInt4LinearPaddedGroups(64, 16, torch.from_numpy(layer),
+                                    torch.ones(2, 16, dtype=torch.float16),
+                                    torch.zeros(2, 2, dtype=torch.int32), groupsize=32)
+    with pytest.raises(ValueError):  # odd groups are re-laid on the device only
+        FusedInt4LinearPaddedGroups(52, 16, torch.from_numpy(O.pack_rows(np.zeros((52, 16)))),
+                                    torch.ones(2, 16, dtype=torch.float16),
+                                    torch.zeros(2, 2, dtype=torch.int32), groupsize=26)
+
+
+def test_loader_rejects_checkpoint_without_metadata(tmp_path):
+    from safetensors.torch import save_file
+
+    from onecomp_runtime import load_int4_model
+
+    path = tmp_path / "plain.safetensors"
+    save_file({"w": torch.zeros(2)}, str(path))
+    with pytest.raises(ValueError, match="config_json"):
+        load_int4_model(str(path), lambda cfg: torch.nn.Linear(2, 2), device="cpu")
