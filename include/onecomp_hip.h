@@ -52,8 +52,9 @@ extern "C" {
 
 /* ---- GEMM regime selection (oc_int4_gemm `regime`) ---------------------- */
 #define OC_REGIME_AUTO 0
-#define OC_REGIME_SPLITK 1 /* small-M split-K streaming kernel (M <= 64)     */
+#define OC_REGIME_SPLITK 1 /* small-M MFMA kernel, K split over the waves (M <= 64) */
 #define OC_REGIME_TILED 2  /* large-M LDS-tiled MFMA kernel                  */
+#define OC_REGIME_DOT 3    /* decode kernel (M <= 2): VALU dot2, factored scales */
 
 /* Human-readable name of a status code. */
 const char *oc_status_string(int status);
@@ -90,14 +91,40 @@ int oc_int4_plan_groups(const int64_t *g_idx, int32_t K, int32_t groupsize,
                         int32_t *num_groups_out, int32_t *identity_out);
 
 /*
- * Device: re-lay packed rows. Physical row k' of qweight_out [K_phys/8, N]
- * takes the 4-bit code of input row kmap[k'] (zero code when kmap[k'] < 0).
- * Replaces the load-time repacks at layers/fused_int4_linear.py:76-124 and
- * the K padding at :1016-1045. qweight_in is [ceil(K/8), N].
+ * Device, load time: build the tiled layout ("tile16") every GEMM entry
+ * point reads. Output features are cut into tiles of 16; within a tile the
+ * 32-row K steps follow each other, and within a step the 16 columns' 4
+ * packed words are adjacent (one 16-byte load = a whole 32-row group of one
+ * column; a wave instruction reads 1 KB of consecutive bytes):
+ *   qt  int32 [tiles][K_phys/32][16][4]   word (t, ks, c, w) = the codes of
+ *        physical rows 32ks + 8w .. +7 of column 16t + c, where physical row
+ *        k' holds input row kmap[k'] (zero code for -1; kmap NULL = identity
+ *        with rows >= K zero)
+ *   st  16-bit [tiles][G][16]            scale of (group, column 16t + c)
+ *   zt  int32 [tiles][G][2]              8 zero points per word, stored as
+ *        the zero itself (a v1 checkpoint's stored zero-1 is restored here)
+ * tiles = ceil(N/16), G = K_phys / group_rows; columns past N are zero.
+ * Inputs: qweight [ceil(K/8), N], scales [>= G, N], qzeros [>= G, N/8] in
+ * the checkpoint formats (header comment). Replaces the load-time repacks of
+ * layers/fused_int4_linear.py:76-124 (_pack_int4_weights,
+ * _repack_groups_to_32) and the K padding at :1016-1045.
  */
-int oc_int4_repack_rows(const int32_t *qweight_in, int32_t K, int32_t N,
-                        const int32_t *kmap, int32_t K_phys,
-                        int32_t *qweight_out, void *stream);
+int oc_int4_prepare(const int32_t *qweight, int32_t K, int32_t N,
+                    const int32_t *kmap, int32_t K_phys, int32_t group_rows,
+                    const void *scales, int32_t scale_dtype,
+                    const int32_t *qzeros, int32_t zero_mode, int32_t *qt,
+                    void *st, int32_t *zt, void *stream);
+
+/*
+ * Device, test/inspection and the fp32-activation path: dense out[N, K_logical]
+ * (original K order) from the tiled layout, each value RNE_out(s * (code - zero))
+ * exactly as quant_utils.dequant_gptq_to_fp (quant_utils.py:50-69).
+ */
+int oc_int4_dequant_tiled(const int32_t *qt, const void *st,
+                          int32_t scale_dtype, const int32_t *zt,
+                          const int32_t *kmap, int32_t N, int32_t K_phys,
+                          int32_t group_rows, int32_t K_logical, void *out,
+                          int32_t out_dtype, void *stream);
 
 /*
  * Device: unpack int32-packed `wbits` codes along dim 0,
@@ -126,36 +153,39 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
 /*
  * Device: fused int4 dequant + GEMM, C[M, N] = A' @ Wd + bias, where
  *   A'[m, k'] = kmap ? (kmap[k'] >= 0 ? A[m, kmap[k']] : 0) : A[m, k'],
- *   Wd[k', n] = RNE_a( f32(scales[k'/group_rows, n]) * (code(k', n) - zero) )
+ *   Wd[k', n] = RNE_a( f32(scale) * (code(k', n) - zero) )   (see oc_int4_prepare)
  * computed with fp32 accumulation and rounded once to a_dtype on store
- * (bias added in fp32). Replaces the Triton launches of
- * layers/fused_int4_linear.py:1194-1208 (FusedInt4Linear.forward), :504-532
- * (fused_int4_gemm) and :904-919 (FusedInt4LinearPaddedGroups.forward), and
- * the act-order packed path layers/packed_gptq_linear.py:66-74.
- *   a        [M, K_logical] (row stride lda elements), a_dtype in {F16, BF16}
- *   qweight  [K_phys/8, N] int32 (physical rows, see oc_int4_plan_groups)
- *   scales   [K_phys/group_rows, N], scale_dtype in {F16, BF16}
- *   qzeros   [K_phys/group_rows, N/8] int32
- *   kmap     NULL or int32 [K_phys] (device)
+ * (bias added in fp32). The decode regime (M <= 2) evaluates the same sum
+ * with the scale and zero factored out of each 32-row group (exact for a
+ * one-hot row; otherwise equal up to fp32 summation order). Replaces the
+ * Triton launches of layers/fused_int4_linear.py:1194-1208
+ * (FusedInt4Linear.forward), :504-532 (fused_int4_gemm) and :904-919
+ * (FusedInt4LinearPaddedGroups.forward), and the act-order packed path
+ * layers/packed_gptq_linear.py:66-74.
+ *   a        [M, K_logical] (row stride lda elements, lda % 8 == 0, 16-byte
+ *            aligned), a_dtype in {F16, BF16}
+ *   qt/st/zt tiled weights from oc_int4_prepare (scale_dtype F16 or BF16)
+ *   kmap     NULL or int32 [K_phys] (device, 16-byte aligned)
  *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
  *   c        [M, N] (row stride ldc elements) of a_dtype
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
  * K_phys % group_rows == 0; without kmap K_logical == K_phys.
- * The workspace (>= oc_int4_gemm_workspace_bytes) must be zero-filled
- * before its first use; the library leaves it zero-filled after every call,
- * so one workspace serves any sequence of calls on one stream. Calls that
- * overlap in time must not share a workspace.
+ * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned, any
+ * contents) holds gathered activations (kmap with M > 2) and fp32 split-K
+ * partials (large M, few output tiles); calls that overlap in time must not
+ * share a workspace. `regime`: OC_REGIME_*.
  */
 int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
-                 int32_t K_logical, const int32_t *qweight, const void *scales,
-                 int32_t scale_dtype, const int32_t *qzeros, int32_t zero_mode,
-                 int32_t N, int32_t K_phys, int32_t group_rows,
-                 const int32_t *kmap, const void *bias, int32_t bias_dtype,
-                 void *c, int64_t ldc, void *workspace, size_t workspace_bytes,
-                 int32_t regime, void *stream);
+                 int32_t K_logical, const int32_t *qt, const void *st,
+                 int32_t scale_dtype, const int32_t *zt, int32_t N,
+                 int32_t K_phys, int32_t group_rows, const int32_t *kmap,
+                 const void *bias, int32_t bias_dtype, void *c, int64_t ldc,
+                 void *workspace, size_t workspace_bytes, int32_t regime,
+                 void *stream);
 
-/* Workspace bytes oc_int4_gemm needs for this shape (0 if none). */
+/* Workspace bytes oc_int4_gemm needs for this call shape (0 if none). */
 size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys,
+                                    int32_t group_rows, int32_t has_kmap,
                                     int32_t regime);
 
 /*
@@ -217,15 +247,15 @@ int oc_moe_route(const int64_t *topk_ids, int32_t T, int32_t topk, int32_t E,
  * Device: grouped int4 GEMM over E experts (no reference counterpart; see
  * oc_moe_route). For every routed pair p = t*topk + j of expert e:
  *   Y[p, :] = X[t, :] @ Wd_e        (fp32 accumulation, rounded to x_dtype)
- * x [T, K] (row stride ldx) in {F16, BF16}; per-expert GPTQ tensors stacked
- * on a leading E axis: qweight [E, K/8, N], scales [E, K/group_rows, N],
- * qzeros [E, K/group_rows, N/8]; y [T*topk, N] (row stride ldy).
- * K % 32 == 0, group_rows % 32 == 0, N % 64 == 0.
+ * x [T, K] (row stride ldx) in {F16, BF16}; per-expert tiled weights
+ * (oc_int4_prepare of each expert, identity kmap) stacked on a leading E
+ * axis: qt [E][N/16][K/32][16][4], st [E][N/16][G][16], zt [E][N/16][G][2];
+ * y [T*topk, N] (row stride ldy). K % 32 == 0, group_rows % 32 == 0,
+ * N % 64 == 0.
  */
 int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T,
-                     int32_t topk, int32_t K, const int32_t *qweight,
-                     const void *scales, int32_t scale_dtype,
-                     const int32_t *qzeros, int32_t zero_mode,
+                     int32_t topk, int32_t K, const int32_t *qt,
+                     const void *st, int32_t scale_dtype, const int32_t *zt,
                      int32_t group_rows, int32_t E, int32_t N,
                      const int32_t *expert_offsets, const int32_t *sorted_pairs,
                      void *y, int64_t ldy, void *stream);

@@ -80,29 +80,36 @@ __device__ __forceinline__ float load_any_f32(const void *p, int64_t i, int dt) 
 // 16-bit float (<= 11 significant bits) and |w - z| <= 15 the product has at
 // most 15 significant bits, so fp32 holds it exactly.
 //
-// Here each 4-bit code w is turned into the fp16 number 1024 + w by OR-ing it
-// into the mantissa of 0x6400 (= 1024.0h). For a column with scale s and zero
-// z, let c = -s * (1024 + z): both s * (1024 + w) and c need at most 22
-// significant bits, so they are exact in fp32, and the fused multiply-add
-// fma(1024 + w, s, c) (v_fma_mix_f32: the fp16 operand is read directly)
-// produces the exact s * (w - z). One VALU op per weight, plus a shared
-// shift/insert per code pair and one pack per output pair.
+// Each 4-bit code w is placed in the mantissa of the fp16 number 1024.0
+// (bits 0x6400): at bits 0-3 it reads as 1024 + w, at bits 4-7 as 1024 + 16w.
+// With c = -s * (1024 + z) and, for the second form, s16 = s / 16 and
+// c16 = -s * (64 + z), every product s * (1024 + w), s16 * (1024 + 16w) and
+// both constants need at most 22 significant bits, so fma(h, s, c) yields the
+// exact s * (w - z) (v_fma_mix_f32 reads the fp16 operand directly). One
+// shift, four and-or, eight fma and four pack ops dequantize one 8-code word.
+
+// (x & mask) | magic in one VALU op (mask from an SGPR, magic from a VGPR).
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t mask, uint32_t magic) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(mask), "v"(magic));
+  return r;
+}
 
 struct GroupParam {
-  float s;  // scale as fp32 (exact)
-  float c;  // -s * (1024 + zero) (exact)
+  float s;    // scale (exact fp32)
+  float c;    // -s * (1024 + zero)
+  float s16;  // s / 16
+  float c16;  // -s * (64 + zero)
 };
 
 __device__ __forceinline__ GroupParam make_group_param(float s, int zero) {
+  const float zf = static_cast<float>(zero);
   GroupParam p;
   p.s = s;
-  p.c = -s * static_cast<float>(1024 + zero);
+  p.c = -s * (zf + 1024.f);
+  p.s16 = s * 0.0625f;
+  p.c16 = -s * (zf + 64.f);
   return p;
-}
-
-// 4-bit codes at bit positions (4j, 4j+16) -> fp16 pair (1024 + code_j, 1024 + code_{j+4}).
-__device__ __forceinline__ uint32_t magic_pair(uint32_t q_shifted) {
-  return (q_shifted & 0x000F000Fu) | 0x64006400u;
 }
 
 // Dequantize the 8 codes of one packed word (code i at bits 4i) with one
@@ -110,24 +117,44 @@ __device__ __forceinline__ uint32_t magic_pair(uint32_t q_shifted) {
 // (dword d = codes 2d, 2d+1), each rounded once (RNE) to DT.
 template <int DT>
 __device__ __forceinline__ uint4 dequant8(uint32_t q, GroupParam gp) {
-  const v2f16 h0 = bitcast<v2f16>(magic_pair(q));        // codes 0,4
-  const v2f16 h1 = bitcast<v2f16>(magic_pair(q >> 4));   // codes 1,5
-  const v2f16 h2 = bitcast<v2f16>(magic_pair(q >> 8));   // codes 2,6
-  const v2f16 h3 = bitcast<v2f16>(magic_pair(q >> 12));  // codes 3,7
+  const uint32_t magic = 0x64006400u;
+  const uint32_t q8 = q >> 8;
+  const v2f16 h0 = bitcast<v2f16>(and_or(q, 0x000F000Fu, magic));   // 1024 + codes 0, 4
+  const v2f16 h1 = bitcast<v2f16>(and_or(q, 0x00F000F0u, magic));   // 1024 + 16 * codes 1, 5
+  const v2f16 h2 = bitcast<v2f16>(and_or(q8, 0x000F000Fu, magic));  // 1024 + codes 2, 6
+  const v2f16 h3 = bitcast<v2f16>(and_or(q8, 0x00F000F0u, magic));  // 1024 + 16 * codes 3, 7
   const float f0 = __builtin_fmaf(static_cast<float>(h0[0]), gp.s, gp.c);
   const float f4 = __builtin_fmaf(static_cast<float>(h0[1]), gp.s, gp.c);
-  const float f1 = __builtin_fmaf(static_cast<float>(h1[0]), gp.s, gp.c);
-  const float f5 = __builtin_fmaf(static_cast<float>(h1[1]), gp.s, gp.c);
+  const float f1 = __builtin_fmaf(static_cast<float>(h1[0]), gp.s16, gp.c16);
+  const float f5 = __builtin_fmaf(static_cast<float>(h1[1]), gp.s16, gp.c16);
   const float f2 = __builtin_fmaf(static_cast<float>(h2[0]), gp.s, gp.c);
   const float f6 = __builtin_fmaf(static_cast<float>(h2[1]), gp.s, gp.c);
-  const float f3 = __builtin_fmaf(static_cast<float>(h3[0]), gp.s, gp.c);
-  const float f7 = __builtin_fmaf(static_cast<float>(h3[1]), gp.s, gp.c);
+  const float f3 = __builtin_fmaf(static_cast<float>(h3[0]), gp.s16, gp.c16);
+  const float f7 = __builtin_fmaf(static_cast<float>(h3[1]), gp.s16, gp.c16);
   uint4 r;
   r.x = pack2<DT>(f0, f1);
   r.y = pack2<DT>(f2, f3);
   r.z = pack2<DT>(f4, f5);
   r.w = pack2<DT>(f6, f7);
   return r;
+}
+
+// ---- tiled GPTQ layout ("tile16") ---------------------------------------------
+//
+// Built once per layer by oc_int4_prepare. Output features are cut into tiles
+// of 16; within a tile the 32-row K steps follow each other, and within a K
+// step the 16 columns' 4 packed words (rows 8w..8w+7 of the step, w = 0..3)
+// are adjacent, so one 16-byte load gives a lane a whole 32-row group of one
+// column and a wave reads 1 KB of consecutive bytes per instruction:
+//   word(t, ks, c, w)   qt[((t * KS + ks) * 16 + c) * 4 + w]
+//   scale(t, g, c)      st[(t * G + g) * 16 + c]
+//   zero word(t, g, h)  zt[(t * G + g) * 2 + h]   (columns 8h..8h+7, stored
+//                                                   as the zero itself)
+// KS = K_phys / 32 and G = K_phys / group_rows; columns past N are zero.
+constexpr int TILE_N = 16;
+
+__device__ __forceinline__ int tile_zero(uint32_t zword, int c) {
+  return static_cast<int>((zword >> (4 * (c & 7))) & 0xFu);
 }
 
 // Zero point of column n from a packed qzeros row, with the v1/v2 convention.
@@ -179,11 +206,6 @@ __device__ __forceinline__ v4f32 mfma16x16x32(uint4 a, uint4 b, v4f32 acc) {
   } else {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(bitcast<v8f16>(a), bitcast<v8f16>(b), acc, 0, 0, 0);
   }
-}
-
-// Agent-scope relaxed load that bypasses the (non-coherent) per-CU L1.
-__device__ __forceinline__ float load_coherent(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace oc

@@ -1,19 +1,19 @@
 // Fused int4 dequant + GEMM kernels for gfx950 and their host dispatch.
 //
-// Two regimes:
-//  * split-K streaming kernel (M <= 64): every lane streams 16-byte chunks of
-//    packed weights (4 adjacent columns x 8 K rows), dequantizes them in
-//    registers and feeds v_mfma_f32_16x16x32 with the activation rows as the
-//    A operand. Waves of a workgroup split K and reduce through LDS; the
-//    workgroups of one column tile split K further and the last one to finish
-//    reduces their fp32 partials in a fixed order (deterministic).
-//  * LDS-tiled kernel (large M): a workgroup owns a BM x BN output tile; the
-//    activation tile for each 32-row K step is staged in LDS (double
-//    buffered) and shared by the 4 waves, which split BN; each wave
-//    dequantizes only its own columns, once per K step, straight into MFMA
-//    B operands (no weight re-dequant across waves).
-// Both use dequant8() (exact fp32 product, one RNE to the activation type),
-// the same routine the standalone dequant kernel is tested with.
+// GPTQ weights are read in the tiled layout built by oc_int4_prepare (tile16,
+// oc_device.h): every wave instruction streams 1 KB of consecutive bytes and
+// a lane receives whole 32-row groups of a column. Three regimes:
+//  * decode (M <= 2): VALU dot products with the scale/zero factored out of
+//    each 32-row group (v_dot2_f32_{bf16,f16}); HBM-bound by construction.
+//  * small M (M <= 64): v_mfma_f32_16x16x32 with one lane load feeding four
+//    MFMAs (the four 8-row octets of a group); K is split over the waves of a
+//    workgroup, which owns one 16-column tile (no cross-workgroup results).
+//  * large M: LDS-tiled MFMA GEMM; the activation tile of each 32-row step is
+//    shared through LDS by 4 waves that split the columns, and each wave
+//    dequantizes only its own columns once per step.
+// The MFMA regimes dequantize with dequant8() (exact fp32 product, one RNE to
+// the activation type). Act-order / padded-group layers gather activations
+// into physical row order first (decode does it while staging into LDS).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -31,10 +31,9 @@ struct GemmParams {
   int64_t lda;
   int M;
   int K_logical;
-  const void *qw;      // GPTQ: int32 [K_phys/8, N]; RTN: uint8 [N, row_bytes]
-  const void *scales;  // GPTQ: [G, N] 16-bit; RTN: [N, G] of scale_dtype
-  const void *zeros;   // GPTQ: int32 [G, N/8]; RTN: [N, G] of zero_dtype
-  int zero_mode;       // GPTQ
+  const void *qw;      // GPTQ: tile16 words; RTN: uint8 [N, row_bytes]
+  const void *scales;  // GPTQ: tile16 16-bit scales; RTN: [N, G] of scale_dtype
+  const void *zeros;   // GPTQ: tile16 zero words; RTN: [N, G] of zero_dtype
   int scale_dtype;     // RTN (runtime)
   int zero_dtype;      // RTN (runtime)
   int rtn_gs;          // RTN: columns per group
@@ -42,87 +41,34 @@ struct GemmParams {
   int row_bytes;       // RTN
   int N;
   int K_phys;
+  int KS;              // K_phys / 32
+  int G;               // K_phys / group_rows
   int group_rows;
-  const int32_t *kmap;
+  int gshift;          // log2(group_rows / 32), or -1
+  const int32_t *kmap;  // decode kernel only (the MFMA regimes get gathered activations)
   const void *bias;
   int bias_dtype;
   void *c;
   int64_t ldc;
-  float *partials;    // [ksplit, M, N] fp32 (split-K only)
-  int32_t *counters;  // one per output tile (split-K only), zero on entry and exit
+  float *partials;  // [ksplit, M, N] fp32 (large-M split-K only)
   int ksplit;
   int ksteps_per_split;
   // grouped (MoE) launch
   const int32_t *expert_offsets;
   const int32_t *sorted_pairs;
   int topk;
-  int64_t qw_expert_stride;  // elements of qw per expert
-  int64_t s_expert_stride;
-  int64_t z_expert_stride;
+  int64_t qw_expert_stride;  // 32-bit words per expert
+  int64_t s_expert_stride;   // 16-bit scales per expert
+  int64_t z_expert_stride;   // zero words per expert
 };
 
-// ---------------------------------------------------------------------------
-// Weight access, per format.
-
-// Packed word (8 codes, code i at bits 4i) of column n, K rows 8*wrow .. 8*wrow+7.
-template <int FMT>
-__device__ __forceinline__ uint32_t load_word(const GemmParams &p, const void *qw, int wrow, int n) {
-  if constexpr (FMT == FMT_GPTQ) {
-    return static_cast<const uint32_t *>(qw)[static_cast<int64_t>(wrow) * p.N + n];
-  } else {
-    return *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(qw) +
-                                               static_cast<int64_t>(n) * p.row_bytes + 4 * wrow);
-  }
+__device__ __forceinline__ int group_of(const GemmParams &p, int ks) {
+  return p.gshift >= 0 ? (ks >> p.gshift) : (32 * ks) / p.group_rows;
 }
 
 template <int SDT>
-__device__ __forceinline__ GroupParam gptq_param(const GemmParams &p, const void *scales,
-                                                 const void *zeros, int g, int n) {
-  const uint16_t sb = static_cast<const uint16_t *>(scales)[static_cast<int64_t>(g) * p.N + n];
-  const float s = SDT == OC_DTYPE_BF16 ? bf16_to_f32(sb) : f16_to_f32(sb);
-  const uint32_t zw =
-      static_cast<const uint32_t *>(zeros)[static_cast<int64_t>(g) * (p.N >> 3) + (n >> 3)];
-  return make_group_param(s, unpack_zero(zw, n, p.zero_mode));
-}
-
-template <int DT>
-__device__ __forceinline__ RtnParam rtn_param(const GemmParams &p, int g, int n) {
-  const int64_t i = static_cast<int64_t>(n) * p.rtn_G + g;
-  RtnParam r;
-  r.zq = round_to<DT>(load_any_f32(p.zeros, i, p.zero_dtype));
-  r.sq = round_to<DT>(load_any_f32(p.scales, i, p.scale_dtype));
-  return r;
-}
-
-// Dequantized B operand (8 K rows of column n starting at row 8*wrow).
-template <int DT, int SDT, int FMT>
-__device__ __forceinline__ uint4 load_b(const GemmParams &p, const void *qw, const void *scales,
-                                        const void *zeros, int wrow, int n) {
-  const uint32_t q = load_word<FMT>(p, qw, wrow, n);
-  if constexpr (FMT == FMT_GPTQ) {
-    const int g = (8 * wrow) / p.group_rows;
-    return dequant8<DT>(q, gptq_param<SDT>(p, scales, zeros, g, n));
-  } else {
-    const int g = (8 * wrow) / p.rtn_gs;
-    return rtn_dequant8<DT>(q, rtn_param<DT>(p, g, n));
-  }
-}
-
-// 8 activation values of row `row`, physical K rows k0 .. k0+7.
-template <bool KMAP>
-__device__ __forceinline__ uint4 load_a8(const GemmParams &p, const uint16_t *arow, int k0) {
-  if constexpr (!KMAP) {
-    return *reinterpret_cast<const uint4 *>(arow + k0);
-  } else {
-    uint32_t h[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int src = p.kmap[k0 + e];
-      h[e] = src >= 0 ? arow[src] : 0u;
-    }
-    return make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
-                      h[6] | (h[7] << 16));
-  }
+__device__ __forceinline__ float scale_f32(uint32_t bits) {
+  return SDT == OC_DTYPE_BF16 ? bf16_to_f32(static_cast<uint16_t>(bits)) : f16_to_f32(static_cast<uint16_t>(bits));
 }
 
 template <int DT>
@@ -134,177 +80,389 @@ __device__ __forceinline__ float bias_at(const GemmParams &p, int n) {
   return p.bias ? load_any_f32(p.bias, n, p.bias_dtype) : 0.f;
 }
 
-// Split-K completion: returns true in every thread of the workgroup that
-// finished last for counter `tile` (after all partial stores are visible).
-__device__ __forceinline__ bool splitk_arrive(const GemmParams &p, int tile, int *s_flag) {
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const int prev = atomicAdd(p.counters + tile, 1);
-    *s_flag = prev == p.ksplit - 1;
-  }
-  __syncthreads();
-  const bool last = *s_flag != 0;
-  if (last) __threadfence();
-  return last;
-}
-
-__device__ __forceinline__ void splitk_reset(const GemmParams &p, int tile) {
-  if (threadIdx.x == 0) __hip_atomic_store(p.counters + tile, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Workgroup order -> tile, keeping neighbouring tiles on one XCD (workgroups
+// are handed to the 8 XCDs round-robin); identity unless 8 divides the count.
+__device__ __forceinline__ int xcd_block(int bid, int nblocks) {
+  if (nblocks % 8 != 0) return bid;
+  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
 }
 
 // ---------------------------------------------------------------------------
-// Split-K streaming kernel. grid = (ceil(N/64), ksplit); 256 threads.
-// Lane (quad = l/16, c16 = l%16) of a wave owns columns n0 + 4*c16 + j
-// (j = 0..3, one 16-byte load per K step) and K rows 32*ks + 8*quad + 0..7.
-// MFMA j therefore computes the columns {n0 + 4*i + j : i = 0..15}.
-template <int DT, int SDT, int MT, bool KMAP, int FMT>
-__global__ __launch_bounds__(256) void gemv_splitk_kernel(GemmParams p) {
-  constexpr int WAVES = 4;
-  __shared__ float red[WAVES][MT * 16][65];
-  __shared__ int s_last;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int quad = lane >> 4, c16 = lane & 15;
-  const int n0 = blockIdx.x * 64;
-  const int ncol = n0 + 4 * c16;
-  const bool col_ok = ncol < p.N;
-  const int ksteps = p.K_phys / 32;
-  const int ks_begin = blockIdx.y * p.ksteps_per_split;
-  const int ks_end = min(ks_begin + p.ksteps_per_split, ksteps);
+// Decode kernel (M <= 2). grid = tiles, 256 threads. Lane (c = l%16, h = l/16)
+// of wave w owns column 16t + c and the K steps lp, lp+16, ... (lp = 4w + h),
+// so each wave instruction reads four consecutive K steps of the tile (1 KB).
+//
+// The scale and zero are factored out of each 32-row group:
+//   sum_k x_k * s * (w_k - z) = s * (sum_k x_k * (B + w_k) - (B + z) * sum_k x_k)
+// where B + w_k is the exact 16-bit number made by OR-ing the 4-bit code into
+// the mantissa of B (bf16 128.0 / fp16 1024.0). The first sum runs on
+// v_dot2_f32_{bf16,f16} (fp32 accumulation) against activation pairs staged
+// once per workgroup in LDS (permuted by kmap, interleaved to match the code
+// pairs (i, i+4) of a packed word), the second from per-step activation sums
+// staged beside them.
+constexpr int DOT_PF = 8;
+
+template <int DT>
+__device__ __forceinline__ float dot2acc(uint32_t b, uint32_t x, float acc) {
+  if constexpr (DT == OC_DTYPE_BF16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(bitcast<v2bf16>(b), bitcast<v2bf16>(x), acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(bitcast<v2f16>(b), bitcast<v2f16>(x), acc, false);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint32_t h16) {
+  if constexpr (DT == OC_DTYPE_BF16) return bf16_to_f32(static_cast<uint16_t>(h16));
+  else return f16_to_f32(static_cast<uint16_t>(h16));
+}
+
+size_t dot_lds_bytes(int MR, int KS) {
+  return static_cast<size_t>(MR) * KS * (4 * sizeof(uint4) + sizeof(float2));
+}
+
+template <int DT, int SDT, int MR, bool KMAP>
+__global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
+  constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
+  constexpr float BASE = DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
+  extern __shared__ __attribute__((aligned(16))) uint4 dot_lds[];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int c = lane & 15, h = lane >> 4;
+  const int lp = 4 * wave + h;
+  const int t = xcd_block(blockIdx.x, gridDim.x);
+  const int n = TILE_N * t + c;
+  const int KS = p.KS, M = p.M;
+  uint4 *xpairs = dot_lds;                                          // [MR][KS * 4]
+  float2 *xsum = reinterpret_cast<float2 *>(dot_lds + MR * KS * 4);  // [MR][KS]: (sum, BASE * sum)
+  const uint4 *qt4 = static_cast<const uint4 *>(p.qw) + static_cast<int64_t>(t) * KS * TILE_N + c;
+  const uint16_t *stp = static_cast<const uint16_t *>(p.scales) + static_cast<int64_t>(t) * p.G * TILE_N + c;
+  const uint32_t *ztp = static_cast<const uint32_t *>(p.zeros) + static_cast<int64_t>(t) * p.G * 2 + (c >> 3);
+
+  struct Stage {
+    uint4 q;
+    uint32_t s;
+    uint32_t z;
+  };
+  Stage st[DOT_PF];
+  auto load = [&](Stage &S, int ks) {
+    S.q = qt4[ks * TILE_N];
+    const int g = ks >> p.gshift;
+    S.s = stp[g * TILE_N];
+    S.z = ztp[g * 2];
+  };
+#pragma unroll
+  for (int f = 0; f < DOT_PF; ++f) {
+    const int ks = lp + 16 * f;
+    if (ks < KS) load(st[f], ks);
+  }
+
+  // Stage activations: one thread per K step and row.
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
-
-  v4f32 acc[MT][4];
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+    const uint16_t *arow = a + static_cast<int64_t>(m) * p.lda;
+    for (int ks = tid; ks < KS; ks += blockDim.x) {
+      uint32_t v[32];
+      if constexpr (KMAP) {
+        int src[32];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
-
-  for (int ks = ks_begin + wave; ks < ks_end; ks += WAVES) {
-    const int wrow = 4 * ks + quad;
-    uint4 b[4];
-    if (col_ok) {
-      if constexpr (FMT == FMT_GPTQ) {
-        const uint4 q = *reinterpret_cast<const uint4 *>(static_cast<const uint32_t *>(p.qw) +
-                                                         static_cast<int64_t>(wrow) * p.N + ncol);
-        const int g = (32 * ks) / p.group_rows;
-        const uint2 sr = *reinterpret_cast<const uint2 *>(static_cast<const uint16_t *>(p.scales) +
-                                                          static_cast<int64_t>(g) * p.N + ncol);
-        const uint32_t zw = static_cast<const uint32_t *>(p.zeros)[static_cast<int64_t>(g) * (p.N >> 3) + (ncol >> 3)];
-        const uint16_t sb[4] = {static_cast<uint16_t>(sr.x), static_cast<uint16_t>(sr.x >> 16),
-                                static_cast<uint16_t>(sr.y), static_cast<uint16_t>(sr.y >> 16)};
-        const uint32_t qs[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float s = SDT == OC_DTYPE_BF16 ? bf16_to_f32(sb[j]) : f16_to_f32(sb[j]);
-          b[j] = dequant8<DT>(qs[j], make_group_param(s, unpack_zero(zw, ncol + j, p.zero_mode)));
+        for (int i = 0; i < 8; ++i) {
+          const int4 k4 = *reinterpret_cast<const int4 *>(p.kmap + 32 * ks + 4 * i);
+          src[4 * i] = k4.x; src[4 * i + 1] = k4.y; src[4 * i + 2] = k4.z; src[4 * i + 3] = k4.w;
         }
+        // Rows without a source (-1, or anything outside [0, K_logical)) read as zero.
+        uint32_t g[32];
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          if (static_cast<unsigned>(src[i]) >= static_cast<unsigned>(p.K_logical)) src[i] = -1;
+          g[i] = arow[max(src[i], 0)];
+        }
+#pragma unroll
+        for (int i = 0; i < 32; ++i) v[i] = src[i] >= 0 ? g[i] : 0u;
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = load_b<DT, SDT, FMT>(p, p.qw, p.scales, p.zeros, wrow, ncol + j);
+        for (int i = 0; i < 4; ++i) {
+          const uint4 raw = *reinterpret_cast<const uint4 *>(arow + 32 * ks + 8 * i);
+          v[8 * i + 0] = raw.x & 0xFFFFu; v[8 * i + 1] = raw.x >> 16;
+          v[8 * i + 2] = raw.y & 0xFFFFu; v[8 * i + 3] = raw.y >> 16;
+          v[8 * i + 4] = raw.z & 0xFFFFu; v[8 * i + 5] = raw.z >> 16;
+          v[8 * i + 6] = raw.w & 0xFFFFu; v[8 * i + 7] = raw.w >> 16;
+        }
       }
-    } else {
+      float sum = 0.f;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = make_uint4(0, 0, 0, 0);
-    }
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t *o = v + 8 * w;
+        xpairs[(m * KS + ks) * 4 + w] =
+            make_uint4(o[0] | (o[4] << 16), o[1] | (o[5] << 16), o[2] | (o[6] << 16), o[3] | (o[7] << 16));
 #pragma unroll
-    for (int t = 0; t < MT; ++t) {
-      const int row = 16 * t + c16;
-      uint4 av = make_uint4(0, 0, 0, 0);
-      if (row < p.M) av = load_a8<KMAP>(p, a + static_cast<int64_t>(row) * p.lda, 32 * ks + 8 * quad);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
+        for (int i = 0; i < 8; ++i) sum += half_to_f32<DT>(o[i]);
+      }
+      xsum[m * KS + ks] = make_float2(sum, BASE * sum);
     }
   }
-
-  // Cross-wave reduction. Lane value acc[t][j][i] is row 16t + 4*quad + i,
-  // local column 4*c16 + j.
-#pragma unroll
-  for (int t = 0; t < MT; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 16 * t + 4 * quad + i;
-        if (row < p.M) red[wave][row][4 * c16 + j] = acc[t][j][i];
-      }
   __syncthreads();
 
-  const int M = p.M;
-  if (p.ksplit == 1) {
-    for (int e = tid; e < M * 64; e += 256) {
-      const int row = e >> 6, col = e & 63, n = n0 + col;
-      if (n >= p.N) continue;
-      const float v = red[0][row][col] + red[1][row][col] + red[2][row][col] + red[3][row][col];
-      store_c<DT>(p.c, static_cast<int64_t>(row) * p.ldc + n, v + bias_at(p, n));
+  float acc[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+  const uint32_t magic = MAGIC;
+  for (int base = lp; base < KS; base += 16 * DOT_PF) {
+#pragma unroll
+    for (int f = 0; f < DOT_PF; ++f) {
+      const int ks = base + 16 * f;
+      if (ks >= KS) break;
+      const Stage cur = st[f];
+      if (ks + 16 * DOT_PF < KS) load(st[f], ks + 16 * DOT_PF);
+      float d[MR];
+#pragma unroll
+      for (int m = 0; m < MR; ++m) d[m] = 0.f;
+      const uint32_t qs[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t q = qs[w];
+        const uint32_t b0 = and_or(q, 0x000F000Fu, magic);
+        const uint32_t b1 = and_or(q >> 4, 0x000F000Fu, magic);
+        const uint32_t b2 = and_or(q >> 8, 0x000F000Fu, magic);
+        const uint32_t b3 = and_or(q >> 12, 0x000F000Fu, magic);
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+          const uint4 xp = xpairs[(m * KS + ks) * 4 + w];
+          d[m] = dot2acc<DT>(b0, xp.x, d[m]);
+          d[m] = dot2acc<DT>(b1, xp.y, d[m]);
+          d[m] = dot2acc<DT>(b2, xp.z, d[m]);
+          d[m] = dot2acc<DT>(b3, xp.w, d[m]);
+        }
+      }
+      const float zf = static_cast<float>(tile_zero(cur.z, c));
+      const float s = scale_f32<SDT>(cur.s);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        const float2 xs = xsum[m * KS + ks];
+        acc[m] = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, d[m] - xs.y), acc[m]);
+      }
     }
-    return;
   }
-  float *part = p.partials + static_cast<int64_t>(blockIdx.y) * M * p.N;
-  for (int e = tid; e < M * 64; e += 256) {
-    const int row = e >> 6, col = e & 63, n = n0 + col;
-    if (n >= p.N) continue;
-    part[static_cast<int64_t>(row) * p.N + n] =
-        red[0][row][col] + red[1][row][col] + red[2][row][col] + red[3][row][col];
+
+  // Phases h of one wave (xor 16, 32), then the 4 waves through LDS in order.
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    acc[m] += __shfl_xor(acc[m], 16);
+    acc[m] += __shfl_xor(acc[m], 32);
   }
-  if (!splitk_arrive(p, blockIdx.x, &s_last)) return;
-  for (int e = tid; e < M * 64; e += 256) {
-    const int row = e >> 6, col = e & 63, n = n0 + col;
-    if (n >= p.N) continue;
-    float v = 0.f;
-    for (int s = 0; s < p.ksplit; ++s)
-      v += load_coherent(p.partials + (static_cast<int64_t>(s) * M + row) * p.N + n);
-    store_c<DT>(p.c, static_cast<int64_t>(row) * p.ldc + n, v + bias_at(p, n));
+  __syncthreads();
+  float(*red)[MR][TILE_N] = reinterpret_cast<float(*)[MR][TILE_N]>(dot_lds);
+  if (h == 0) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) red[wave][m][c] = acc[m];
   }
-  splitk_reset(p, blockIdx.x);
+  __syncthreads();
+  if (wave != 0 || h != 0 || n >= p.N) return;
+  const float bv = bias_at(p, n);
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    if (m >= M) break;
+    const float v = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+    store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bv);
+  }
 }
 
 // ---------------------------------------------------------------------------
-// LDS-tiled kernel. BM = 16*WM rows, BN = 64*WN columns (4 waves x 16*WN).
+// Small-M MFMA kernel (M <= 64). grid = tiles, 256 threads; wave w takes the
+// quad-steps (4 K steps) w, w+4, ... of the tile. Lane (quad = l/16, c16 =
+// l%16) loads the 4 words of column c16 for K step 4*qs + quad (one 16-byte
+// load; the wave reads 1 KB of consecutive bytes) and feeds MFMA j with word
+// j: MFMA j's K dimension runs over octet j of the 4 K steps, and the A
+// operand of lane (quad, r) is x[r, 32*(4qs + quad) + 8j .. +7] to match. One
+// group parameter per lane covers 32 weights.
+template <int DT, int SDT, int MT>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemmParams p) {
+  constexpr int PF = 4;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int quad = lane >> 4, c16 = lane & 15;
+  const int t = xcd_block(blockIdx.x, gridDim.x);
+  const int n = TILE_N * t + c16;
+  const int KS = p.KS, M = p.M;
+  const int QS = (KS + 3) / 4;
+  const uint4 *qt4 = static_cast<const uint4 *>(p.qw) + static_cast<int64_t>(t) * KS * TILE_N + c16;
+  const uint16_t *stp = static_cast<const uint16_t *>(p.scales) + static_cast<int64_t>(t) * p.G * TILE_N + c16;
+  const uint32_t *ztp = static_cast<const uint32_t *>(p.zeros) + static_cast<int64_t>(t) * p.G * 2 + (c16 >> 3);
+  const uint16_t *a = static_cast<const uint16_t *>(p.a);
+
+  struct Stage {
+    uint4 q;
+    uint32_t s;
+    uint32_t z;
+  };
+  Stage st[PF];
+  auto load = [&](Stage &S, int qs) {
+    const int ks = 4 * qs + quad;
+    if (ks < KS) {
+      S.q = qt4[ks * TILE_N];
+      const int g = group_of(p, ks);
+      S.s = stp[g * TILE_N];
+      S.z = ztp[g * 2];
+    } else {
+      S.q = make_uint4(0, 0, 0, 0);
+      S.s = 0;
+      S.z = 0;
+    }
+  };
+  auto load_a = [&](uint4 (&av)[MT][4], int qs) {
+    const int ks = 4 * qs + quad;
+#pragma unroll
+    for (int tt = 0; tt < MT; ++tt) {
+      const int row = 16 * tt + c16;
+      const bool ok = row < M && ks < KS;
+      const uint16_t *src = a + static_cast<int64_t>(row) * p.lda + 32 * ks;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        av[tt][j] = ok ? *reinterpret_cast<const uint4 *>(src + 8 * j) : make_uint4(0, 0, 0, 0);
+    }
+  };
+#pragma unroll
+  for (int f = 0; f < PF; ++f) {
+    const int qs = wave + 4 * f;
+    if (qs < QS) load(st[f], qs);
+  }
+  v4f32 acc[MT];
+#pragma unroll
+  for (int tt = 0; tt < MT; ++tt) acc[tt] = v4f32{0.f, 0.f, 0.f, 0.f};
+  uint4 av[MT][4];
+  if (wave < QS) load_a(av, wave);
+
+  for (int base = wave; base < QS; base += 4 * PF) {
+#pragma unroll
+    for (int f = 0; f < PF; ++f) {
+      const int qs = base + 4 * f;
+      if (qs >= QS) break;
+      const Stage cur = st[f];
+      uint4 a_cur[MT][4];
+#pragma unroll
+      for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a_cur[tt][j] = av[tt][j];
+      if (qs + 4 < QS) load_a(av, qs + 4);
+      if (qs + 4 * PF < QS) load(st[f], qs + 4 * PF);
+      const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c16));
+      const uint32_t qwords[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint4 b = dequant8<DT>(qwords[j], gp);
+#pragma unroll
+        for (int tt = 0; tt < MT; ++tt) acc[tt] = mfma16x16x32<DT>(a_cur[tt][j], b, acc[tt]);
+      }
+    }
+  }
+
+  // acc[tt][i] = row 16tt + 4*quad + i, column c16. Fixed LDS tree over the 4 waves.
+  __shared__ float red[2][MT * 16][TILE_N + 1];
+#pragma unroll
+  for (int half = 2; half >= 1; half >>= 1) {
+    if (wave >= half && wave < 2 * half) {
+#pragma unroll
+      for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) red[wave - half][16 * tt + 4 * quad + i][c16] = acc[tt][i];
+    }
+    __syncthreads();
+    if (wave < half) {
+#pragma unroll
+      for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[tt][i] += red[wave][16 * tt + 4 * quad + i][c16];
+    }
+    __syncthreads();
+  }
+  if (wave != 0 || n >= p.N) return;
+  const float bv = bias_at(p, n);
+#pragma unroll
+  for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 16 * tt + 4 * quad + i;
+      if (row < M) store_c<DT>(p.c, static_cast<int64_t>(row) * p.ldc + n, acc[tt][i] + bv);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Weight access of the large-M kernel, per format.
+template <int FMT>
+__device__ __forceinline__ uint32_t load_word(const GemmParams &p, const void *qw, int tile, int ks, int quad,
+                                              int c16) {
+  if constexpr (FMT == FMT_GPTQ) {
+    return static_cast<const uint32_t *>(qw)[((static_cast<int64_t>(tile) * p.KS + ks) * TILE_N + c16) * 4 + quad];
+  } else {
+    const int n = TILE_N * tile + c16;
+    return *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(qw) +
+                                               static_cast<int64_t>(n) * p.row_bytes + 16 * ks + 4 * quad);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ RtnParam rtn_param(const GemmParams &p, int g, int n) {
+  const int64_t i = static_cast<int64_t>(n) * p.rtn_G + g;
+  RtnParam r;
+  r.zq = round_to<DT>(load_any_f32(p.zeros, i, p.zero_dtype));
+  r.sq = round_to<DT>(load_any_f32(p.scales, i, p.scale_dtype));
+  return r;
+}
+
+// Sum of the split-K partials in split order, plus bias, rounded once.
+template <int DT>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t MN = static_cast<int64_t>(p.M) * p.N;
+  if (idx >= MN) return;
+  const int n = static_cast<int>(idx % p.N);
+  const int row = static_cast<int>(idx / p.N);
+  float v = 0.f;
+  for (int s = 0; s < p.ksplit; ++s) v += p.partials[s * MN + idx];
+  store_c<DT>(p.c, static_cast<int64_t>(row) * p.ldc + n, v + bias_at(p, n));
+}
+
+// ---------------------------------------------------------------------------
+// LDS-tiled kernel. BM = 16*WM rows, BN = 64*WN columns (4 waves x WN tiles).
 // grid = (ceil(N/BN), ceil(M/BM), ksplit) or, grouped, (ceil(N/BN), 1, E).
 constexpr int A_LDS_STRIDE = 40;  // halves per LDS row: 32 data + 8 pad (80 B)
 
-template <int DT, int SDT, int WM, int WN, bool KMAP, int FMT, bool MOE>
+template <int DT, int SDT, int WM, int WN, int FMT, bool MOE>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   constexpr int BM = 16 * WM;
   constexpr int BN = 64 * WN;
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * A_LDS_STRIDE];
-  __shared__ int s_last;
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int n0 = blockIdx.x * BN;
-  const int nw = n0 + wave * 16 * WN;  // first column of this wave
+  const int tw = n0 / TILE_N + wave * WN;  // first tile of this wave
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
 
   const void *qw = p.qw;
   const void *scales = p.scales;
   const void *zeros = p.zeros;
-  int row_begin = 0, row_end = p.M, m_first;
+  int row_end = p.M, m_first;
   if constexpr (MOE) {
     const int e = blockIdx.z;
-    row_begin = p.expert_offsets[e];
+    m_first = p.expert_offsets[e];
     row_end = p.expert_offsets[e + 1];
     qw = static_cast<const uint32_t *>(p.qw) + e * p.qw_expert_stride;
     scales = static_cast<const uint16_t *>(p.scales) + e * p.s_expert_stride;
     zeros = static_cast<const uint32_t *>(p.zeros) + e * p.z_expert_stride;
-    m_first = row_begin;
   } else {
     m_first = blockIdx.y * BM;
   }
-  const int ksteps = p.K_phys / 32;
-  int ks_begin = 0, ks_end = ksteps;
+  int ks_begin = 0, ks_end = p.KS;
   if constexpr (!MOE) {
     ks_begin = blockIdx.z * p.ksteps_per_split;
-    ks_end = min(ks_begin + p.ksteps_per_split, ksteps);
+    ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
   }
 
-  // Activation staging: chunk c = (row, 16-byte piece) of the BM x 32 tile.
   constexpr int A_CHUNKS = BM * 4;
   constexpr int A_PER_THREAD = (A_CHUNKS + 255) / 256;
 
   for (int m0 = m_first; m0 < (MOE ? row_end : m_first + 1); m0 += BM) {
-    // Source row pointer of each staged chunk (null = zero row).
     const uint16_t *src_row[A_PER_THREAD];
 #pragma unroll
     for (int i = 0; i < A_PER_THREAD; ++i) {
@@ -321,7 +479,8 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 #pragma unroll
       for (int i = 0; i < A_PER_THREAD; ++i) {
         const int ch = tid + 256 * i;
-        areg[i] = src_row[i] ? load_a8<KMAP>(p, src_row[i], 32 * ks + 8 * (ch & 3)) : make_uint4(0, 0, 0, 0);
+        areg[i] = src_row[i] ? *reinterpret_cast<const uint4 *>(src_row[i] + 32 * ks + 8 * (ch & 3))
+                             : make_uint4(0, 0, 0, 0);
       }
     };
     auto store_a_tile = [&](int buf, const uint4 (&areg)[A_PER_THREAD]) {
@@ -332,22 +491,26 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
           *reinterpret_cast<uint4 *>(&As[buf][(ch >> 2) * A_LDS_STRIDE + 8 * (ch & 3)]) = areg[i];
       }
     };
-    // Weight words and group parameters of the next K step, per column subtile.
     uint32_t qreg[WN];
     auto load_w = [&](int ks) {
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        const int n = nw + 16 * j + c16;
-        qreg[j] = n < p.N ? load_word<FMT>(p, qw, 4 * ks + quad, n) : 0u;
+        const int n = TILE_N * (tw + j) + c16;
+        qreg[j] = n < p.N ? load_word<FMT>(p, qw, tw + j, ks, quad, c16) : 0u;
       }
     };
     auto dequant_w = [&](int ks, uint4 (&b)[WN]) {
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        const int n = min(nw + 16 * j + c16, p.N - 1);
         if constexpr (FMT == FMT_GPTQ) {
-          b[j] = dequant8<DT>(qreg[j], gptq_param<SDT>(p, scales, zeros, (32 * ks) / p.group_rows, n));
+          const int g = group_of(p, ks);
+          const int tl = min(tw + j, (p.N - 1) / TILE_N);  // keep metadata reads inside the tensor
+          const int64_t tgs = static_cast<int64_t>(tl) * p.G + g;
+          const uint16_t sb = static_cast<const uint16_t *>(scales)[tgs * TILE_N + c16];
+          const uint32_t zw = static_cast<const uint32_t *>(zeros)[tgs * 2 + (c16 >> 3)];
+          b[j] = dequant8<DT>(qreg[j], make_group_param(scale_f32<SDT>(sb), tile_zero(zw, c16)));
         } else {
+          const int n = min(TILE_N * (tw + j) + c16, p.N - 1);
           b[j] = rtn_dequant8<DT>(qreg[j], rtn_param<DT>(p, (32 * ks + 8 * quad) / p.rtn_gs, n));
         }
       }
@@ -385,7 +548,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
       __syncthreads();
     }
 
-    // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column nw + 16j + c16.
+    // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
     if constexpr (MOE) {
 #pragma unroll
       for (int t = 0; t < WM; ++t)
@@ -396,14 +559,14 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
           const int64_t orow = p.sorted_pairs[r];
 #pragma unroll
           for (int j = 0; j < WN; ++j) {
-            const int n = nw + 16 * j + c16;
+            const int n = TILE_N * (tw + j) + c16;
             if (n < p.N) store_c<DT>(p.c, orow * p.ldc + n, acc[t][j][i]);
           }
         }
     } else if (p.ksplit == 1) {
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        const int n = nw + 16 * j + c16;
+        const int n = TILE_N * (tw + j) + c16;
         if (n >= p.N) continue;
         const float bv = bias_at(p, n);
 #pragma unroll
@@ -415,10 +578,11 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
           }
       }
     } else {
+      // split-K: fp32 partials; splitk_reduce_kernel sums them in split order
       float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
-        const int n = nw + 16 * j + c16;
+        const int n = TILE_N * (tw + j) + c16;
         if (n >= p.N) continue;
 #pragma unroll
         for (int t = 0; t < WM; ++t)
@@ -428,26 +592,6 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
             if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
           }
       }
-      const int tile = blockIdx.y * gridDim.x + blockIdx.x;
-      if (!splitk_arrive(p, tile, &s_last)) return;
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const int n = nw + 16 * j + c16;
-        if (n >= p.N) continue;
-        const float bv = bias_at(p, n);
-#pragma unroll
-        for (int t = 0; t < WM; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = m0 + 16 * t + 4 * quad + i;
-            if (r >= p.M) continue;
-            float v = 0.f;
-            for (int s = 0; s < p.ksplit; ++s)
-              v += load_coherent(p.partials + (static_cast<int64_t>(s) * p.M + r) * p.N + n);
-            store_c<DT>(p.c, static_cast<int64_t>(r) * p.ldc + n, v + bv);
-          }
-      }
-      splitk_reset(p, tile);
     }
   }
 }
@@ -516,34 +660,50 @@ int env_int(const char *name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
-struct SplitPlan {
+int ilog2_exact(int v) {
+  if (v <= 0 || (v & (v - 1)) != 0) return -1;
+  int s = 0;
+  while ((1 << s) < v) ++s;
+  return s;
+}
+
+size_t align256(size_t v) { return (v + 255) / 256 * 256; }
+
+struct Plan {
   int regime;
-  int mt;         // split-K: row tiles of 16
-  TileCfg tile;   // tiled
+  int mt;        // small-M kernel: row tiles of 16
+  TileCfg tile;  // large-M kernel
   int ksplit;
   int ksteps_per_split;
-  int tiles;      // counters needed
+  bool gather;   // activations gathered into physical order first (kmap, MFMA regimes)
 };
 
-SplitPlan plan_gemm(int M, int N, int K_phys, int regime) {
-  SplitPlan sp{};
+// The decode kernel takes M <= 2, power-of-two groups of 32-row steps and its
+// activation rows in (at most 128 KB of) LDS.
+bool dot_eligible(int M, int K_phys, int group_rows) {
+  return M >= 1 && M <= 2 && ilog2_exact(group_rows / 32) >= 0 && dot_lds_bytes(M, K_phys / 32) <= 128 * 1024;
+}
+
+Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime) {
+  Plan sp{};
   const int ksteps = K_phys / 32;
-  if (regime == OC_REGIME_AUTO) regime = M <= 64 ? OC_REGIME_SPLITK : OC_REGIME_TILED;
+  // Tuning knobs, read once per process.
+  static const bool dot_disabled = env_int("ONECOMP_HIP_DISABLE_DOT", 0) != 0;
+  static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
+  if (regime == OC_REGIME_AUTO) {
+    if (!dot_disabled && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
+    else regime = M <= 64 ? OC_REGIME_SPLITK : OC_REGIME_TILED;
+  }
   sp.regime = regime;
+  sp.ksplit = 1;
+  sp.ksteps_per_split = ksteps;
+  sp.gather = has_kmap && regime != OC_REGIME_DOT;
+  if (regime == OC_REGIME_DOT) return sp;
   if (regime == OC_REGIME_SPLITK) {
     sp.mt = std::max(1, (M + 15) / 16);
-    const int col_tiles = (N + 63) / 64;
-    const int target = env_int("ONECOMP_HIP_SPLITK_TARGET_WGS", 1024);
-    const int min_ksteps = env_int("ONECOMP_HIP_SPLITK_MIN_KSTEPS", 8);
-    int ksplit = (target + col_tiles - 1) / col_tiles;
-    ksplit = std::max(1, std::min(ksplit, std::max(1, ksteps / std::max(1, min_ksteps))));
-    sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
-    sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
-    sp.tiles = col_tiles;
     return sp;
   }
   static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
-  const int want = env_int("ONECOMP_HIP_TILED_MIN_WGS", 256);
   TileCfg pick = cfgs[2];
   for (const TileCfg &c : cfgs) {
     const int64_t tiles = static_cast<int64_t>((M + 16 * c.wm - 1) / (16 * c.wm)) *
@@ -559,99 +719,77 @@ SplitPlan plan_gemm(int M, int N, int K_phys, int regime) {
   if (tiles < want) ksplit = std::min((want + tiles - 1) / tiles, std::max(1, ksteps / 8));
   sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
   sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
-  sp.tiles = tiles;
   return sp;
 }
 
-size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
-
-size_t workspace_bytes(const SplitPlan &sp, int M, int N) {
-  if (sp.ksplit <= 1) return 0;
-  return align_up(static_cast<size_t>(sp.tiles) * 4, 256) +
-         static_cast<size_t>(sp.ksplit) * M * N * sizeof(float);
+// Workspace: [gathered activations (bf16/fp16, M x K_phys)][split-K partials].
+size_t gather_bytes(const Plan &sp, int M, int K_phys) {
+  return sp.gather ? align256(static_cast<size_t>(M) * K_phys * 2) : 0;
+}
+size_t workspace_bytes(const Plan &sp, int M, int N, int K_phys) {
+  size_t b = gather_bytes(sp, M, K_phys);
+  if (sp.ksplit > 1) b += static_cast<size_t>(sp.ksplit) * M * N * sizeof(float);
+  return b;
 }
 
-template <int DT, int SDT, int MT, bool KMAP, int FMT>
-void launch_splitk_t(const GemmParams &p, int col_tiles, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_splitk_kernel<DT, SDT, MT, KMAP, FMT>), dim3(col_tiles, p.ksplit), dim3(256), 0,
-                     s, p);
+template <int DT, int SDT, int MR, bool KMAP>
+void launch_dot_t(const GemmParams &p, hipStream_t s) {
+  auto kern = gemv_dot_kernel<DT, SDT, MR, KMAP>;
+  static bool attr_set = false;  // once per instantiation: allow up to 128 KB of dynamic LDS
+  if (!attr_set) {
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              128 * 1024);
+    attr_set = true;
+  }
+  const size_t lds = std::max(dot_lds_bytes(MR, p.KS), sizeof(float) * 4 * MR * TILE_N);
+  hipLaunchKernelGGL(kern, dim3((p.N + TILE_N - 1) / TILE_N), dim3(256), lds, s, p);
 }
 
-template <int DT, int SDT, bool KMAP, int FMT>
-void launch_splitk_mt(const GemmParams &p, int mt, int col_tiles, hipStream_t s) {
+template <int DT, int SDT>
+void launch_dot(const GemmParams &p, hipStream_t s) {
+  const bool km = p.kmap != nullptr;
+  if (p.M == 1) km ? launch_dot_t<DT, SDT, 1, true>(p, s) : launch_dot_t<DT, SDT, 1, false>(p, s);
+  else km ? launch_dot_t<DT, SDT, 2, true>(p, s) : launch_dot_t<DT, SDT, 2, false>(p, s);
+}
+
+template <int DT, int SDT, int MT>
+void launch_mfma_t(const GemmParams &p, hipStream_t s) {
+  hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT>), dim3((p.N + TILE_N - 1) / TILE_N), dim3(256), 0, s, p);
+}
+
+template <int DT, int SDT>
+void launch_mfma(const GemmParams &p, int mt, hipStream_t s) {
   switch (mt) {
-    case 1: launch_splitk_t<DT, SDT, 1, KMAP, FMT>(p, col_tiles, s); break;
-    case 2: launch_splitk_t<DT, SDT, 2, KMAP, FMT>(p, col_tiles, s); break;
-    case 3: launch_splitk_t<DT, SDT, 3, KMAP, FMT>(p, col_tiles, s); break;
-    default: launch_splitk_t<DT, SDT, 4, KMAP, FMT>(p, col_tiles, s); break;
+    case 1: launch_mfma_t<DT, SDT, 1>(p, s); break;
+    case 2: launch_mfma_t<DT, SDT, 2>(p, s); break;
+    case 3: launch_mfma_t<DT, SDT, 3>(p, s); break;
+    default: launch_mfma_t<DT, SDT, 4>(p, s); break;
   }
 }
 
-template <int DT, int SDT, int WM, int WN, bool KMAP, int FMT>
+template <int DT, int SDT, int WM, int WN, int FMT>
 void launch_tiled_t(const GemmParams &p, hipStream_t s) {
   const dim3 grid((p.N + 64 * WN - 1) / (64 * WN), (p.M + 16 * WM - 1) / (16 * WM), p.ksplit);
-  hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, KMAP, FMT, false>), grid, dim3(256), 0, s, p);
-}
-
-template <int DT, int SDT, bool KMAP, int FMT>
-void launch_tiled_cfg(const GemmParams &p, TileCfg c, hipStream_t s) {
-  if (c.wm == 16 && c.wn == 3) launch_tiled_t<DT, SDT, 16, 3, KMAP, FMT>(p, s);
-  else if (c.wm == 8 && c.wn == 2) launch_tiled_t<DT, SDT, 8, 2, KMAP, FMT>(p, s);
-  else launch_tiled_t<DT, SDT, 4, 1, KMAP, FMT>(p, s);
-}
-
-template <int DT, int SDT, bool KMAP, int FMT>
-void launch_plan(const GemmParams &p, const SplitPlan &sp, hipStream_t s) {
-  if (sp.regime == OC_REGIME_SPLITK) launch_splitk_mt<DT, SDT, KMAP, FMT>(p, sp.mt, sp.tiles, s);
-  else launch_tiled_cfg<DT, SDT, KMAP, FMT>(p, sp.tile, s);
-}
-
-template <int FMT>
-void launch_dispatch(const GemmParams &p, const SplitPlan &sp, int a_dtype, int scale_dtype, bool kmap,
-                     hipStream_t s) {
-  // RTN parameters are read with their runtime dtypes; only the activation
-  // type is a template parameter there.
-  const bool bf = a_dtype == OC_DTYPE_BF16;
-  if constexpr (FMT == FMT_RTN) {
-    bf ? launch_plan<OC_DTYPE_BF16, OC_DTYPE_F16, false, FMT>(p, sp, s)
-       : launch_plan<OC_DTYPE_F16, OC_DTYPE_F16, false, FMT>(p, sp, s);
-    return;
-  }
-  const bool sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf) {
-    if (sbf) {
-      kmap ? launch_plan<OC_DTYPE_BF16, OC_DTYPE_BF16, true, FMT>(p, sp, s)
-           : launch_plan<OC_DTYPE_BF16, OC_DTYPE_BF16, false, FMT>(p, sp, s);
-    } else {
-      kmap ? launch_plan<OC_DTYPE_BF16, OC_DTYPE_F16, true, FMT>(p, sp, s)
-           : launch_plan<OC_DTYPE_BF16, OC_DTYPE_F16, false, FMT>(p, sp, s);
-    }
-  } else {
-    if (sbf) {
-      kmap ? launch_plan<OC_DTYPE_F16, OC_DTYPE_BF16, true, FMT>(p, sp, s)
-           : launch_plan<OC_DTYPE_F16, OC_DTYPE_BF16, false, FMT>(p, sp, s);
-    } else {
-      kmap ? launch_plan<OC_DTYPE_F16, OC_DTYPE_F16, true, FMT>(p, sp, s)
-           : launch_plan<OC_DTYPE_F16, OC_DTYPE_F16, false, FMT>(p, sp, s);
-    }
+  hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, false>), grid, dim3(256), 0, s, p);
+  if (p.ksplit > 1) {
+    const int64_t mn = static_cast<int64_t>(p.M) * p.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
+                       s, p);
   }
 }
 
-int attach_workspace(GemmParams &p, const SplitPlan &sp, void *workspace, size_t workspace_bytes_given) {
-  p.ksplit = sp.ksplit;
-  p.ksteps_per_split = sp.ksteps_per_split;
-  p.partials = nullptr;
-  p.counters = nullptr;
-  if (sp.ksplit <= 1) return OC_OK;
-  const size_t need = workspace_bytes(sp, p.M, p.N);
-  if (!workspace || workspace_bytes_given < need)
-    return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
-                workspace ? workspace_bytes_given : static_cast<size_t>(0));
-  if (!aligned(workspace, 256)) return fail(OC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
-  p.counters = static_cast<int32_t *>(workspace);
-  p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                         align_up(static_cast<size_t>(sp.tiles) * 4, 256));
-  return OC_OK;
+template <int DT, int SDT, int FMT>
+void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
+  if (c.wm == 16 && c.wn == 3) launch_tiled_t<DT, SDT, 16, 3, FMT>(p, s);
+  else if (c.wm == 8 && c.wn == 2) launch_tiled_t<DT, SDT, 8, 2, FMT>(p, s);
+  else launch_tiled_t<DT, SDT, 4, 1, FMT>(p, s);
+}
+
+template <int DT, int SDT>
+void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
+  if (sp.regime == OC_REGIME_DOT) launch_dot<DT, SDT>(p, s);
+  else if (sp.regime == OC_REGIME_SPLITK) launch_mfma<DT, SDT>(p, sp.mt, s);
+  else launch_tiled<DT, SDT, FMT_GPTQ>(p, sp.tile, s);
 }
 
 }  // namespace oc
@@ -660,28 +798,25 @@ using namespace oc;
 
 extern "C" {
 
-size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t regime) {
-  if (M <= 0 || N <= 0 || K_phys <= 0) return 0;
-  return workspace_bytes(plan_gemm(M, N, K_phys, regime), M, N);
+size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap,
+                                    int32_t regime) {
+  if (M <= 0 || N <= 0 || K_phys <= 0 || group_rows <= 0) return 0;
+  return workspace_bytes(plan_gemm(M, N, K_phys, group_rows, has_kmap != 0, regime), M, N, K_phys);
 }
 
-int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical,
-                 const int32_t *qweight, const void *scales, int32_t scale_dtype,
-                 const int32_t *qzeros, int32_t zero_mode, int32_t N, int32_t K_phys,
-                 int32_t group_rows, const int32_t *kmap, const void *bias, int32_t bias_dtype,
-                 void *c, int64_t ldc, void *workspace, size_t workspace_bytes_given, int32_t regime,
-                 void *stream) {
+int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
+                 const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
+                 int32_t group_rows, const int32_t *kmap, const void *bias, int32_t bias_dtype, void *c,
+                 int64_t ldc, void *workspace, size_t workspace_bytes_given, int32_t regime, void *stream) {
   clear_error();
   if (M < 0 || N <= 0 || K_phys <= 0 || K_logical <= 0)
     return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K_logical=%d K_phys=%d", M, N, K_logical, K_phys);
   if (M == 0) return OC_OK;
-  if (!a || !qweight || !scales || !qzeros || !c) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!a || !qt || !st || !zt || !c) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (!is_half_dtype(a_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "a_dtype must be F16 or BF16");
   if (!is_half_dtype(scale_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "scale_dtype must be F16 or BF16");
-  if (zero_mode != OC_ZERO_V1 && zero_mode != OC_ZERO_V2)
-    return fail(OC_ERR_INVALID_ARGUMENT, "zero_mode must be OC_ZERO_V1 or OC_ZERO_V2");
   if (bias && !is_float_dtype(bias_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "bad bias dtype");
-  if (regime < OC_REGIME_AUTO || regime > OC_REGIME_TILED)
+  if (regime < OC_REGIME_AUTO || regime > OC_REGIME_DOT)
     return fail(OC_ERR_INVALID_ARGUMENT, "unknown regime %d", regime);
   if (N % 8 != 0) return fail(OC_ERR_SHAPE, "N must be a multiple of 8 (qzeros packing), got N=%d", N);
   if (K_phys % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 || K_phys % group_rows != 0)
@@ -690,42 +825,69 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   if (!kmap && K_logical != K_phys)
     return fail(OC_ERR_SHAPE, "K_logical=%d != K_phys=%d requires a kmap", K_logical, K_phys);
   if (lda < K_logical || ldc < N) return fail(OC_ERR_SHAPE, "lda/ldc smaller than the row length");
-  if (!kmap && (lda % 8 != 0 || !aligned(a, 16)))
-    return fail(OC_ERR_SHAPE, "activations need 16-byte aligned rows (lda %% 8 == 0) without kmap");
-  if (!aligned(qweight, 16) || !aligned(scales, 8) || !aligned(qzeros, 4))
-    return fail(OC_ERR_SHAPE, "qweight must be 16-byte and scales 8-byte aligned");
+  if (lda % 8 != 0 || !aligned(a, 16))
+    return fail(OC_ERR_SHAPE, "activations need 16-byte aligned rows (lda %% 8 == 0)");
+  if (!aligned(qt, 16) || !aligned(kmap, 16)) return fail(OC_ERR_SHAPE, "qweight and kmap must be 16-byte aligned");
+  const int64_t tiles = (N + TILE_N - 1) / TILE_N;
+  if (tiles * (K_phys / 32) * 64 >= (1LL << 31))
+    return fail(OC_ERR_UNSUPPORTED, "layer too large for 32-bit tile offsets");
   if (regime == OC_REGIME_SPLITK && M > 64)
-    return fail(OC_ERR_UNSUPPORTED, "split-K regime supports M <= 64, got M=%d", M);
+    return fail(OC_ERR_UNSUPPORTED, "small-M regime supports M <= 64, got M=%d", M);
+  if (regime == OC_REGIME_DOT && !dot_eligible(M, K_phys, group_rows))
+    return fail(OC_ERR_UNSUPPORTED,
+                "decode regime needs M <= 2, group_rows/32 a power of two and M*K_phys*2.25 B of LDS <= 128 KB "
+                "(M=%d K_phys=%d group_rows=%d)",
+                M, K_phys, group_rows);
 
-  const SplitPlan sp = plan_gemm(M, N, K_phys, regime);
+  const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime);
+  const size_t need = workspace_bytes(sp, M, N, K_phys);
+  if (need > 0) {
+    if (!workspace || workspace_bytes_given < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                  workspace ? workspace_bytes_given : static_cast<size_t>(0));
+    if (!aligned(workspace, 256)) return fail(OC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
   GemmParams p{};
   p.a = a;
   p.lda = lda;
   p.M = M;
   p.K_logical = K_logical;
-  p.qw = qweight;
-  p.scales = scales;
-  p.zeros = qzeros;
-  p.zero_mode = zero_mode;
+  p.qw = qt;
+  p.scales = st;
+  p.zeros = zt;
   p.N = N;
   p.K_phys = K_phys;
+  p.KS = K_phys / 32;
+  p.G = K_phys / group_rows;
   p.group_rows = group_rows;
-  p.kmap = kmap;
+  p.gshift = ilog2_exact(group_rows / 32);
+  p.kmap = sp.regime == OC_REGIME_DOT ? kmap : nullptr;
   p.bias = bias;
   p.bias_dtype = bias_dtype;
   p.c = c;
   p.ldc = ldc;
-  const int ws = attach_workspace(p, sp, workspace, workspace_bytes_given);
-  if (ws != OC_OK) return ws;
-  launch_dispatch<FMT_GPTQ>(p, sp, a_dtype, scale_dtype, kmap != nullptr, static_cast<hipStream_t>(stream));
+  p.ksplit = sp.ksplit;
+  p.ksteps_per_split = sp.ksteps_per_split;
+  if (sp.gather) {
+    launch_gather_cols(a, lda, M, K_logical, kmap, K_phys, workspace, stream);
+    p.a = workspace;
+    p.lda = K_phys;
+  }
+  if (sp.ksplit > 1)
+    p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + gather_bytes(sp, M, K_phys));
+  const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
+  if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);
+  else if (bf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_F16>(p, sp, s);
+  else if (sbf) launch_gptq<OC_DTYPE_F16, OC_DTYPE_BF16>(p, sp, s);
+  else launch_gptq<OC_DTYPE_F16, OC_DTYPE_F16>(p, sp, s);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
 
-int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_t K,
-                  const uint8_t *qweight_u8, int32_t row_bytes, const void *scales, int32_t scale_dtype,
-                  const void *zeros, int32_t zero_dtype, int32_t G, int32_t N, const void *bias,
-                  int32_t bias_dtype, void *c, int64_t ldc, void *stream) {
+int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_t K, const uint8_t *qweight_u8,
+                  int32_t row_bytes, const void *scales, int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
+                  int32_t G, int32_t N, const void *bias, int32_t bias_dtype, void *c, int64_t ldc, void *stream) {
   clear_error();
   if (M < 0 || N <= 0 || K <= 0 || G <= 0) return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K=%d G=%d", M, N, K, G);
   if (M == 0) return OC_OK;
@@ -744,11 +906,14 @@ int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_
     return fail(OC_ERR_SHAPE, "x needs 16-byte aligned rows and qweight 4-byte aligned rows");
 
   // Bias is rounded to the activation type first (`bias.to(x.dtype)`); the
-  // kernels add it in fp32, which is exact for a 16-bit value.
-  SplitPlan sp = plan_gemm(M, N, K, OC_REGIME_AUTO);
-  if (sp.ksplit > 1) {  // no workspace in this entry point
-    sp.ksplit = 1;
-    sp.ksteps_per_split = K / 32;
+  // kernel adds it in fp32, which is exact for a 16-bit value.
+  static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
+  TileCfg pick = cfgs[2];
+  for (const TileCfg &t : cfgs) {
+    if (static_cast<int64_t>((M + 16 * t.wm - 1) / (16 * t.wm)) * ((N + 64 * t.wn - 1) / (64 * t.wn)) >= 256) {
+      pick = t;
+      break;
+    }
   }
   GemmParams p{};
   p.a = x;
@@ -765,14 +930,18 @@ int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_
   p.row_bytes = row_bytes;
   p.N = N;
   p.K_phys = K;
+  p.KS = K / 32;
   p.group_rows = 32;
+  p.gshift = 0;
   p.bias = bias;
   p.bias_dtype = bias_dtype;
   p.c = c;
   p.ldc = ldc;
   p.ksplit = 1;
-  p.ksteps_per_split = sp.ksteps_per_split;
-  launch_dispatch<FMT_RTN>(p, sp, x_dtype, OC_DTYPE_F16, false, static_cast<hipStream_t>(stream));
+  p.ksteps_per_split = K / 32;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (x_dtype == OC_DTYPE_BF16) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN>(p, pick, s);
+  else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_RTN>(p, pick, s);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
@@ -785,42 +954,44 @@ int oc_moe_route(const int64_t *topk_ids, int32_t T, int32_t topk, int32_t E, in
     return fail(OC_ERR_SHAPE, "unsupported routing shape T=%d topk=%d E=%d", T, topk, E);
   const size_t lds = sizeof(int32_t) * (ROUTE_THREADS + 1) * E;
   if (lds > 160 * 1024) return fail(OC_ERR_UNSUPPORTED, "too many experts for one workgroup (E=%d)", E);
-  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(ROUTE_THREADS), lds, static_cast<hipStream_t>(stream),
-                     topk_ids, T * topk, E, expert_offsets, sorted_pairs);
+  if (lds > 64 * 1024)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void *>(moe_route_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+  hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(ROUTE_THREADS), lds, static_cast<hipStream_t>(stream), topk_ids,
+                     T * topk, E, expert_offsets, sorted_pairs);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
 
 int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T, int32_t topk, int32_t K,
-                     const int32_t *qweight, const void *scales, int32_t scale_dtype, const int32_t *qzeros,
-                     int32_t zero_mode, int32_t group_rows, int32_t E, int32_t N,
-                     const int32_t *expert_offsets, const int32_t *sorted_pairs, void *y, int64_t ldy,
-                     void *stream) {
+                     const int32_t *qt, const void *st, int32_t scale_dtype, const int32_t *zt, int32_t group_rows,
+                     int32_t E, int32_t N, const int32_t *expert_offsets, const int32_t *sorted_pairs, void *y,
+                     int64_t ldy, void *stream) {
   clear_error();
   if (T < 0 || topk <= 0 || K <= 0 || E <= 0 || N <= 0) return fail(OC_ERR_SHAPE, "bad shape");
   if (T == 0) return OC_OK;
-  if (!x || !qweight || !scales || !qzeros || !expert_offsets || !sorted_pairs || !y)
+  if (!x || !qt || !st || !zt || !expert_offsets || !sorted_pairs || !y)
     return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (!is_half_dtype(x_dtype) || !is_half_dtype(scale_dtype))
     return fail(OC_ERR_INVALID_ARGUMENT, "x and scales must be F16 or BF16");
-  if (zero_mode != OC_ZERO_V1 && zero_mode != OC_ZERO_V2)
-    return fail(OC_ERR_INVALID_ARGUMENT, "zero_mode must be OC_ZERO_V1 or OC_ZERO_V2");
   if (K % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 || K % group_rows != 0 || N % 64 != 0)
     return fail(OC_ERR_SHAPE, "need K %% 32 == 0, group_rows | K (multiple of 32), N %% 64 == 0");
-  if (ldx % 8 != 0 || !aligned(x, 16) || ldx < K || ldy < N)
-    return fail(OC_ERR_SHAPE, "x needs 16-byte aligned rows");
+  if (ldx % 8 != 0 || !aligned(x, 16) || ldx < K || ldy < N) return fail(OC_ERR_SHAPE, "x needs 16-byte aligned rows");
+  const int64_t tiles = N / TILE_N;
   GemmParams p{};
   p.a = x;
   p.lda = ldx;
   p.M = T * topk;
   p.K_logical = K;
-  p.qw = qweight;
-  p.scales = scales;
-  p.zeros = qzeros;
-  p.zero_mode = zero_mode;
+  p.qw = qt;
+  p.scales = st;
+  p.zeros = zt;
   p.N = N;
   p.K_phys = K;
+  p.KS = K / 32;
+  p.G = K / group_rows;
   p.group_rows = group_rows;
+  p.gshift = ilog2_exact(group_rows / 32);
   p.c = y;
   p.ldc = ldy;
   p.ksplit = 1;
@@ -828,21 +999,21 @@ int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T, int
   p.expert_offsets = expert_offsets;
   p.sorted_pairs = sorted_pairs;
   p.topk = topk;
-  p.qw_expert_stride = static_cast<int64_t>(K / 8) * N;
-  p.s_expert_stride = static_cast<int64_t>(K / group_rows) * N;
-  p.z_expert_stride = static_cast<int64_t>(K / group_rows) * (N / 8);
+  p.qw_expert_stride = tiles * p.KS * 64;
+  p.s_expert_stride = tiles * p.G * TILE_N;
+  p.z_expert_stride = tiles * p.G * 2;
   constexpr int WM = 6, WN = 4;
   const dim3 grid((N + 64 * WN - 1) / (64 * WN), 1, E);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = x_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
   if (bf && sbf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_BF16, WM, WN, false, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_BF16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
   else if (bf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_F16, WM, WN, false, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_F16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
   else if (sbf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_BF16, WM, WN, false, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_BF16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_F16, WM, WN, false, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_F16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }

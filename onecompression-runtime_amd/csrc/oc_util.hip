@@ -1,6 +1,6 @@
 // Status/error API, the host-side group-layout planner, and the
-// memory-bound kernels of the library: packed-row re-layout, GPTQ and RTN
-// dequant to a dense weight, and the packed RTN embedding gather.
+// memory-bound kernels on checkpoint-format tensors: integer unpack, GPTQ and
+// RTN dequant to a dense weight, and the packed RTN embedding gather.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -26,31 +26,6 @@ int fail(int status, const char *fmt, ...) {
 }
 
 void clear_error() { g_last_error[0] = 0; }
-
-// ---------------------------------------------------------------------------
-// Packed-row re-layout: out word (r, n) collects the codes of input rows
-// kmap[8r + i] (zero code for kmap < 0). kmap == NULL means identity with
-// rows >= K zero (pure K padding).
-__global__ __launch_bounds__(256) void repack_rows_kernel(const int32_t *__restrict__ qin, int K,
-                                                          int N, const int32_t *__restrict__ kmap,
-                                                          int K_phys, int32_t *__restrict__ qout) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  const int64_t total = static_cast<int64_t>(K_phys / 8) * N;
-  if (idx >= total) return;
-  const int n = static_cast<int>(idx % N);
-  const int r = static_cast<int>(idx / N);
-  uint32_t word = 0;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int kp = 8 * r + i;
-    const int src = kmap ? kmap[kp] : (kp < K ? kp : -1);
-    if (src >= 0 && src < K) {
-      const uint32_t w = static_cast<uint32_t>(qin[static_cast<int64_t>(src >> 3) * N + n]);
-      word |= ((w >> (4 * (src & 7))) & 0xFu) << (4 * i);
-    }
-  }
-  qout[idx] = static_cast<int32_t>(word);
-}
 
 // ---------------------------------------------------------------------------
 // Integer unpack along dim 0 (see oc_unpack_rows).
@@ -289,21 +264,6 @@ int oc_int4_plan_groups(const int64_t *g_idx, int32_t K, int32_t groupsize, int3
                   static_cast<long long>(kmap_capacity), static_cast<long long>(k_phys));
     std::memcpy(kmap_out, kmap.data(), sizeof(int32_t) * k_phys);
   }
-  return OC_OK;
-}
-
-int oc_int4_repack_rows(const int32_t *qweight_in, int32_t K, int32_t N, const int32_t *kmap,
-                        int32_t K_phys, int32_t *qweight_out, void *stream) {
-  clear_error();
-  if (!qweight_in || !qweight_out) return fail(OC_ERR_INVALID_ARGUMENT, "NULL qweight");
-  if (K <= 0 || N <= 0 || K_phys <= 0 || K_phys % 8 != 0)
-    return fail(OC_ERR_SHAPE, "bad shape K=%d N=%d K_phys=%d (K_phys %% 8 == 0 required)", K, N,
-                K_phys);
-  const int64_t total = static_cast<int64_t>(K_phys / 8) * N;
-  hipLaunchKernelGGL(repack_rows_kernel, dim3(grid_for(total)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), qweight_in, K, N, kmap, K_phys,
-                     qweight_out);
-  OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
 

@@ -13,6 +13,7 @@ device, the call raises.
 from __future__ import annotations
 
 import ctypes
+import functools
 import os
 import threading
 from pathlib import Path
@@ -38,6 +39,7 @@ OC_ZERO_V2 = 2
 OC_REGIME_AUTO = 0
 OC_REGIME_SPLITK = 1
 OC_REGIME_TILED = 2
+OC_REGIME_DOT = 3
 
 LIB_PATH = Path(
     os.environ.get("ONECOMP_HIP_LIB", Path(__file__).resolve().parent / "_lib" / "libonecomp_hip.so")
@@ -65,7 +67,14 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _I32, _I32, _P, _I64, _P, _P, _P, _P],
     ),
-    "oc_int4_repack_rows": (ctypes.c_int, [_P, _I32, _I32, _P, _I32, _P, _P]),
+    "oc_int4_prepare": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _P, _P],
+    ),
+    "oc_int4_dequant_tiled": (
+        ctypes.c_int,
+        [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _P, _I32, _P],
+    ),
     "oc_unpack_rows": (ctypes.c_int, [_P, _I32, _I32, _I32, _I32, _P, _P]),
     "oc_int4_dequant": (
         ctypes.c_int,
@@ -73,10 +82,10 @@ SIGNATURES = {
     ),
     "oc_int4_gemm": (
         ctypes.c_int,
-        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _P, _P, _I32,
+        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _I32,
          _P, _I64, _P, _SZ, _I32, _P],
     ),
-    "oc_int4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "oc_int4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "oc_rtn_dequant": (
         ctypes.c_int,
         [_P, _I32, _I32, _P, _I32, _P, _I32, _I32, _I32, _P, _I32, _P],
@@ -93,7 +102,7 @@ SIGNATURES = {
     "oc_moe_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
     "oc_int4_moe_gemm": (
         ctypes.c_int,
-        [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _I32, _P, _P,
+        [_P, _I64, _I32, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P,
          _P, _I64, _P],
     ),
 }
@@ -170,28 +179,39 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
-def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+_raw_stream = torch._C._cuda_getCurrentRawStream
+
+
+def stream_of(device: torch.device | int) -> int:
+    """Raw handle of torch's current HIP stream on ``device``."""
+    idx = device if isinstance(device, int) else (
+        device.index if device.index is not None else torch.cuda.current_device())
+    return _raw_stream(idx)
 
 
 class _Workspace:
-    """Per-device zero-filled scratch for split-K partials and tile counters.
+    """Per-device scratch: gathered activations and split-K partials.
 
-    The kernels leave the counters at zero after every call and overwrite the
-    partials they read, so one workspace serves every call issued on one
-    stream; it grows (re-zeroed) on demand.
+    One workspace serves every call issued on one stream (each call
+    overwrites the partials it reads); it grows on demand. Run a layer once
+    eagerly before a graph capture so captured launches never grow it.
     """
 
     def __init__(self) -> None:
         self._bufs: dict[int, torch.Tensor] = {}
+        # Outgrown buffers stay allocated: a captured graph may still hold their address.
+        self._retired: list[torch.Tensor] = []
 
-    def get(self, device: torch.device, nbytes: int) -> torch.Tensor | None:
+    def get(self, device: torch.device | int, nbytes: int) -> torch.Tensor | None:
         if nbytes == 0:
             return None
-        idx = device.index if device.index is not None else torch.cuda.current_device()
+        idx = device if isinstance(device, int) else (
+            device.index if device.index is not None else torch.cuda.current_device())
         buf = self._bufs.get(idx)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            if buf is not None:
+                self._retired.append(buf)
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
             self._bufs[idx] = buf
         return buf
 
@@ -199,6 +219,12 @@ class _Workspace:
 workspace = _Workspace()
 
 
-def gemm_workspace(device: torch.device, M: int, N: int, K_phys: int, regime: int):
-    nbytes = int(lib().oc_int4_gemm_workspace_bytes(M, N, K_phys, regime))
+@functools.lru_cache(maxsize=4096)
+def gemm_workspace_bytes(M: int, N: int, K_phys: int, group_rows: int, has_kmap: bool, regime: int) -> int:
+    return int(lib().oc_int4_gemm_workspace_bytes(M, N, K_phys, group_rows, int(has_kmap), regime))
+
+
+def gemm_workspace(device: torch.device | int, M: int, N: int, K_phys: int, group_rows: int,
+                   has_kmap: bool, regime: int):
+    nbytes = gemm_workspace_bytes(M, N, K_phys, group_rows, has_kmap, regime)
     return workspace.get(device, nbytes), nbytes

@@ -58,19 +58,63 @@ def plan_groups(in_features: int, groupsize: int, g_idx: torch.Tensor | None = N
     return GroupPlan(k_phys.value, rows.value, ngroups.value, bool(ident.value), kmap)
 
 
-def repack_rows(qweight: torch.Tensor, in_features: int, kmap: torch.Tensor | None,
-                k_phys: int) -> torch.Tensor:
-    """Re-lay packed int4 rows on the device: row k' <- input row kmap[k']."""
-    dev = require_device(qweight, kmap)
-    if qweight.dtype != torch.int32:
-        raise ValueError("qweight must be int32")
-    qweight = qweight.contiguous()
-    N = qweight.shape[1]
-    out = torch.empty((k_phys // 8, N), dtype=torch.int32, device=dev)
+@dataclass
+class TiledWeights:
+    """A GPTQ layer in the tiled device layout of ``oc_int4_prepare``."""
+
+    qt: torch.Tensor  # int32 [tiles, K_phys/32, 16, 4]
+    st: torch.Tensor  # fp16/bf16 [tiles, G, 16]
+    zt: torch.Tensor  # int32 [tiles, G, 2]
+    N: int
+    k_phys: int
+    group_rows: int
+
+
+def prepare(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, *, in_features: int,
+            out_features: int, kmap: torch.Tensor | None, k_phys: int, group_rows: int,
+            v1: bool) -> TiledWeights:
+    """Build the tiled layout on the device (load time): rows permuted by
+    ``kmap`` into uniform groups, zeros restored to their value."""
+    dev = require_device(qweight, scales, qzeros, kmap)
+    if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+        raise ValueError("qweight and qzeros must be int32")
+    if scales.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"scales must be fp16 or bf16, got {scales.dtype}")
+    qweight, scales, qzeros = qweight.contiguous(), scales.contiguous(), qzeros.contiguous()
+    N = int(out_features)
+    tiles = (N + 15) // 16
+    G = k_phys // group_rows
+    if qweight.dim() != 2 or qweight.shape[1] != N or qweight.shape[0] < (int(in_features) + 7) // 8:
+        raise ValueError(f"qweight shape {tuple(qweight.shape)} does not hold {in_features} x {N} codes")
+    if scales.dim() != 2 or scales.shape[1] != N or scales.shape[0] < G:
+        raise ValueError(f"scales shape {tuple(scales.shape)} does not cover {G} groups x {N}")
+    if qzeros.dim() != 2 or qzeros.shape[1] != N // 8 or qzeros.shape[0] < G:
+        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover {G} groups x {N // 8}")
+    if kmap is not None and (kmap.dtype != torch.int32 or kmap.numel() != k_phys):
+        raise ValueError(f"kmap must be int32 with {k_phys} entries")
+    qt = torch.empty((tiles, k_phys // 32, 16, 4), dtype=torch.int32, device=dev)
+    st = torch.empty((tiles, G, 16), dtype=scales.dtype, device=dev)
+    zt = torch.empty((tiles, G, 2), dtype=torch.int32, device=dev)
     check(
-        lib().oc_int4_repack_rows(ptr(qweight), int(in_features), N, ptr(kmap), int(k_phys), ptr(out),
-                                  stream_of(dev)),
-        "oc_int4_repack_rows",
+        lib().oc_int4_prepare(ptr(qweight), int(in_features), N, ptr(kmap), int(k_phys), int(group_rows),
+                              ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
+                              _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, ptr(qt), ptr(st), ptr(zt),
+                              stream_of(dev)),
+        "oc_int4_prepare",
+    )
+    return TiledWeights(qt, st, zt, N, int(k_phys), int(group_rows))
+
+
+def dequant_tiled(w: TiledWeights, kmap: torch.Tensor | None, in_features: int,
+                  dtype: torch.dtype) -> torch.Tensor:
+    """Dense [N, in_features] weight (original K order) from the tiled layout."""
+    dev = require_device(w.qt, kmap)
+    out = torch.empty((w.N, int(in_features)), dtype=dtype, device=dev)
+    check(
+        lib().oc_int4_dequant_tiled(ptr(w.qt), ptr(w.st), dtype_code(w.st.dtype), ptr(w.zt), ptr(kmap), w.N,
+                                    w.k_phys, w.group_rows, int(in_features), ptr(out), dtype_code(dtype),
+                                    stream_of(dev)),
+        "oc_int4_dequant_tiled",
     )
     return out
 
@@ -114,32 +158,53 @@ def int4_dequant(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tens
     return out
 
 
-def int4_gemm(a_2d: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor,
-              *, in_features: int, k_phys: int, group_rows: int, v1: bool,
+def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
               kmap: torch.Tensor | None = None, bias: torch.Tensor | None = None,
               out: torch.Tensor | None = None, regime: int = _hip.OC_REGIME_AUTO) -> torch.Tensor:
-    """C[M, N] = A @ dequant(W) + bias on the HIP device (fp32 accumulation)."""
-    dev = require_device(a_2d, qweight, scales, qzeros, kmap, bias)
-    if a_2d.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"activations must be fp16 or bf16, got {a_2d.dtype}")
-    if a_2d.stride(-1) != 1:
+    """C[M, N] = A @ dequant(W) + bias on the HIP device (fp32 accumulation).
+
+    This is the per-call hot path of every GPTQ layer, kept lean: one
+    device check, one output allocation, one ABI call.
+    """
+    qt = w.qt
+    if not (a_2d.is_cuda and qt.is_cuda):
+        require_device(a_2d, qt)  # raises with the reason
+    idx = a_2d.get_device()
+    if qt.get_device() != idx:
+        raise ValueError(f"activations on cuda:{idx}, weights on cuda:{qt.get_device()}")
+    adt = a_2d.dtype
+    if adt is not torch.bfloat16 and adt is not torch.float16:
+        raise ValueError(f"activations must be fp16 or bf16, got {adt}")
+    if a_2d.stride(-1) != 1 or a_2d.stride(0) % 8 or a_2d.data_ptr() % 16:
         a_2d = a_2d.contiguous()
     M = a_2d.shape[0]
-    N = qweight.shape[1]
+    N = w.N
     if out is None:
-        out = torch.empty((M, N), dtype=a_2d.dtype, device=dev)
-    ws, nbytes = _hip.gemm_workspace(dev, M, N, k_phys, regime)
-    check(
-        lib().oc_int4_gemm(
-            ptr(a_2d), a_2d.stride(0), dtype_code(a_2d.dtype), M, int(in_features), ptr(qweight),
-            ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
-            _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, N, int(k_phys), int(group_rows), ptr(kmap),
-            ptr(bias), dtype_code(bias.dtype) if bias is not None else 0, ptr(out), out.stride(0),
-            ptr(ws), nbytes, int(regime), stream_of(dev),
-        ),
-        "oc_int4_gemm",
+        out = torch.empty((M, N), dtype=adt, device=a_2d.device)
+    ws, nbytes = _hip.gemm_workspace(idx, M, N, w.k_phys, w.group_rows, kmap is not None, regime)
+    status = _gemm_fn()(
+        a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, in_features, qt.data_ptr(), w.st.data_ptr(),
+        _DT[w.st.dtype], w.zt.data_ptr(), N, w.k_phys, w.group_rows,
+        None if kmap is None else kmap.data_ptr(),
+        None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
+        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes, regime,
+        _hip.stream_of(idx),
     )
+    if status:
+        check(status, "oc_int4_gemm")
     return out
+
+
+_DT = {torch.float16: _hip.OC_DTYPE_F16, torch.bfloat16: _hip.OC_DTYPE_BF16,
+       torch.float32: _hip.OC_DTYPE_F32}
+_GEMM_FN = None
+
+
+def _gemm_fn():
+    global _GEMM_FN
+    if _GEMM_FN is None:
+        _GEMM_FN = lib().oc_int4_gemm
+    return _GEMM_FN
 
 
 def rtn_dequant(qweight_u8: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor,
@@ -214,21 +279,36 @@ def moe_route(topk_ids: torch.Tensor, num_experts: int) -> tuple[torch.Tensor, t
     return offsets, sorted_pairs
 
 
-def int4_moe_gemm(x: torch.Tensor, topk: int, qweight: torch.Tensor, scales: torch.Tensor,
-                  qzeros: torch.Tensor, expert_offsets: torch.Tensor, sorted_pairs: torch.Tensor,
-                  *, group_rows: int = 32, v1: bool = True) -> torch.Tensor:
+def prepare_experts(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, *,
+                    group_rows: int = 32, v1: bool = True) -> TiledWeights:
+    """Stacked per-expert GPTQ tensors [E, K/8, N] / [E, G, N] / [E, G, N/8]
+    -> tiled layout with a leading expert axis."""
+    E, K8, N = qweight.shape
+    K = 8 * K8
+    parts = [prepare(qweight[e], scales[e], qzeros[e], in_features=K, out_features=N, kmap=None,
+                     k_phys=K, group_rows=group_rows, v1=v1) for e in range(E)]
+    return TiledWeights(torch.stack([p.qt for p in parts]), torch.stack([p.st for p in parts]),
+                        torch.stack([p.zt for p in parts]), N, K, group_rows)
+
+
+def int4_moe_gemm(x: torch.Tensor, topk: int, w: TiledWeights, expert_offsets: torch.Tensor,
+                  sorted_pairs: torch.Tensor) -> torch.Tensor:
     """Y[t*topk + j, :] = x[t] @ dequant(W_{e(t,j)}) for every routed pair."""
-    dev = require_device(x, qweight, scales, qzeros, expert_offsets, sorted_pairs)
-    x, qweight, scales, qzeros = x.contiguous(), qweight.contiguous(), scales.contiguous(), qzeros.contiguous()
+    dev = require_device(x, w.qt, expert_offsets, sorted_pairs)
+    x = x.contiguous()
     T, K = x.shape
-    E, _, N = qweight.shape
-    y = torch.empty((T * topk, N), dtype=x.dtype, device=dev)
+    E = w.qt.shape[0]
+    if expert_offsets.dtype != torch.int32 or expert_offsets.numel() != E + 1:
+        raise ValueError(f"expert_offsets must be int32 with {E + 1} entries (one expert per weight)")
+    if sorted_pairs.dtype != torch.int32 or sorted_pairs.numel() < T * topk:
+        raise ValueError(f"sorted_pairs must be int32 with {T * topk} entries")
+    if K != w.k_phys:
+        raise ValueError(f"x has {K} features, the experts {w.k_phys}")
+    y = torch.empty((T * topk, w.N), dtype=x.dtype, device=dev)
     check(
-        lib().oc_int4_moe_gemm(ptr(x), x.stride(0), dtype_code(x.dtype), T, int(topk), K,
-                               ptr(qweight), ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
-                               _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, int(group_rows), E, N,
-                               ptr(expert_offsets), ptr(sorted_pairs), ptr(y), y.stride(0),
-                               stream_of(dev)),
+        lib().oc_int4_moe_gemm(ptr(x), x.stride(0), dtype_code(x.dtype), T, int(topk), K, ptr(w.qt), ptr(w.st),
+                               dtype_code(w.st.dtype), ptr(w.zt), int(w.group_rows), E, w.N,
+                               ptr(expert_offsets), ptr(sorted_pairs), ptr(y), y.stride(0), stream_of(dev)),
         "oc_int4_moe_gemm",
     )
     return y

@@ -6,13 +6,16 @@ FusedInt4LinearAnyGroup :639-758). Every forward is one launch of
 ``oc_int4_gemm`` on torch's current stream.
 
 Layout. All classes share one load-time plan (``oc_int4_plan_groups``):
-the packed rows are re-laid on the device into uniform groups of
-``group_rows`` (a multiple of 32) physical rows. For groupsize 32 without
-act-order the plan is the identity and the checkpoint's qweight is used as
-is; odd group sizes get 32-row slots with zero rows (the reference's
-``_repack_groups_to_32``) and the kernel reads the matching activation
-columns through ``kmap`` (the reference's ``src_k`` remap, :370-376);
-act-order ``g_idx`` sorts rows by group. Scales and zeros are never copied.
+the packed rows are re-laid into uniform groups of ``group_rows`` (a
+multiple of 32) physical rows -- odd group sizes get 32-row slots with zero
+rows (the reference's ``_repack_groups_to_32``, :94-124), act-order ``g_idx``
+sorts rows by group -- and ``oc_int4_prepare`` writes the weight once into
+the tiled device layout the kernels stream: 16-column tiles whose 32-row
+steps are 256 contiguous bytes, with the tile's scales and zeros (restored
+to their value, so v1 and v2 checkpoints run the same kernels) beside them.
+The layer keeps only the tiled tensors (``qweight_tiled``, ``scales_tiled``,
+``zeros_tiled``); checkpoint-format tensors given on the CPU are held until
+the first device forward prepares them.
 """
 from __future__ import annotations
 
@@ -50,26 +53,50 @@ class _HipGPTQLinear(torch.nn.Module):
                              f"{plan.num_groups} groups x {self.out_features // 8}")
         self.k_phys = plan.k_phys
         self.group_rows = plan.group_rows
-        if plan.identity:
-            qw_phys = qweight
-            kmap = None
-        else:
-            if not qweight.is_cuda:
-                raise ValueError(
-                    "this layer's packed rows are re-laid out on the HIP device at load time; "
-                    "construct it from device tensors (the backend.build_* helpers do)")
-            kmap = torch.from_numpy(plan.kmap).to(qweight.device)
-            qw_phys = kernels.repack_rows(qweight, self.in_features, kmap, plan.k_phys)
+        self.num_phys_groups = plan.num_groups
         if scales.dtype not in (torch.float16, torch.bfloat16):
             scales = scales.to(torch.float16)
-        self.register_buffer("qweight", qw_phys.contiguous())
-        self.register_buffer("scales", scales.contiguous())
-        self.register_buffer("qzeros", qzeros.contiguous())
+        # The kernels read activations through kmap only when the rows moved.
+        kmap = None if plan.identity else torch.from_numpy(plan.kmap).to(qweight.device)
         self.register_buffer("kmap", kmap, persistent=False)
+        self.register_buffer("qweight_tiled", None)
+        self.register_buffer("scales_tiled", None)
+        self.register_buffer("zeros_tiled", None)
+        # Checkpoint-format tensors waiting for the first device forward.
+        self.register_buffer("_src_qweight", qweight, persistent=False)
+        self.register_buffer("_src_scales", scales, persistent=False)
+        self.register_buffer("_src_qzeros", qzeros, persistent=False)
         if bias is not None:
             self.register_buffer("bias", bias.contiguous())
         else:
             self.bias = None
+        self._weights = None
+        if qweight.is_cuda:
+            self._prepare()
+
+    def _prepare(self) -> kernels.TiledWeights:
+        """Write the tiled layout on the layer's device and drop the sources."""
+        w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
+                            in_features=self.in_features, out_features=self.out_features,
+                            kmap=self.kmap, k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
+        self.qweight_tiled, self.scales_tiled, self.zeros_tiled = w.qt, w.st, w.zt
+        self._src_qweight = self._src_scales = self._src_qzeros = None
+        self._weights = w
+        return w
+
+    def tiled(self) -> kernels.TiledWeights:
+        w = self._weights
+        if w is None or w.qt is not self.qweight_tiled or w.st is not self.scales_tiled:
+            if self.qweight_tiled is None:
+                if not self._src_qweight.is_cuda:
+                    raise RuntimeError(
+                        f"{type(self).__name__} runs on the HIP device; move the layer there first "
+                        f"(its weights are on {self._src_qweight.device})")
+                return self._prepare()
+            w = kernels.TiledWeights(self.qweight_tiled, self.scales_tiled, self.zeros_tiled,
+                                     self.out_features, self.k_phys, self.group_rows)
+            self._weights = w
+        return w
 
     def _gemm(self, x: torch.Tensor) -> torch.Tensor:
         orig_dtype = x.dtype
@@ -80,11 +107,8 @@ class _HipGPTQLinear(torch.nn.Module):
         a_2d = x.reshape(-1, self.in_features)
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
-        c = kernels.int4_gemm(
-            a_2d, self.qweight, self.scales, self.qzeros, in_features=self.in_features,
-            k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1, kmap=self.kmap,
-            bias=self.bias,
-        )
+        c = kernels.int4_gemm(a_2d, self.tiled(), in_features=self.in_features, kmap=self.kmap,
+                              bias=self.bias)
         out = c.reshape(*x.shape[:-1], self.out_features)
         if orig_dtype == torch.float32:
             out = out.to(torch.float32)
@@ -93,16 +117,23 @@ class _HipGPTQLinear(torch.nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self._gemm(x)
 
+    def dequantize(self, dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """Dense [out_features, in_features] weight, values as the reference's
+        ``dequant_gptq_to_fp`` (exact fp32 product, one rounding to dtype)."""
+        return kernels.dequant_tiled(self.tiled(), self.kmap, self.in_features, dtype)
+
     @torch.no_grad()
     def warmup(self, m_values=(32, 128, 256, 1024, 2250)) -> None:
         """Run one forward per M so workspaces are sized before timing.
 
         The kernels are compiled ahead of time; there is no JIT to trigger.
         """
-        device = self.qweight.device
+        ref = self.qweight_tiled if self.qweight_tiled is not None else self._src_qweight
+        device = ref.device
         if device.type != "cuda":
             return
-        dtype = self.scales.dtype if self.scales.dtype in (torch.float16, torch.bfloat16) else torch.float16
+        scales = self.scales_tiled if self.scales_tiled is not None else self._src_scales
+        dtype = scales.dtype if scales.dtype in (torch.float16, torch.bfloat16) else torch.float16
         for m in m_values:
             if m <= 0:
                 continue
@@ -110,18 +141,19 @@ class _HipGPTQLinear(torch.nn.Module):
         torch.cuda.synchronize(device)
 
     def _apply(self, fn, recurse=True):
-        # Keep packed integer buffers int32 across .to(dtype=...) and scales
-        # 16-bit (fused_int4_linear.py:1230-1246).
-        qweight_before, qzeros_before, kmap_before = self.qweight, self.qzeros, self.kmap
+        # Keep integer buffers int32 across .to(dtype=...) and scales 16-bit
+        # (fused_int4_linear.py:1230-1246).
+        before = {n: getattr(self, n) for n in ("qweight_tiled", "zeros_tiled", "kmap", "_src_qweight",
+                                                "_src_qzeros")}
         result = super()._apply(fn, recurse=recurse)
-        if self.qweight.dtype != torch.int32:
-            self.qweight = qweight_before.to(self.qweight.device)
-        if self.qzeros.dtype != torch.int32:
-            self.qzeros = qzeros_before.to(self.qzeros.device)
-        if self.kmap is not None and self.kmap.dtype != torch.int32:
-            self.kmap = kmap_before.to(self.kmap.device)
-        if self.scales.dtype not in (torch.float16, torch.bfloat16):
-            self.scales = self.scales.to(torch.float16)
+        for name, old in before.items():
+            new = getattr(self, name)
+            if new is not None and new.dtype != torch.int32:
+                setattr(self, name, old.to(new.device))
+        for name in ("scales_tiled", "_src_scales"):
+            t = getattr(self, name)
+            if t is not None and t.dtype not in (torch.float16, torch.bfloat16):
+                setattr(self, name, t.to(torch.float16))
         return result
 
     def extra_repr(self) -> str:
@@ -220,8 +252,11 @@ def fused_int4_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor
     assert K % 32 == 0, f"K must be a multiple of 32 (groupsize), got K={K}"
     if bias is not None:
         bias = bias.to(a.dtype)
-    c = kernels.int4_gemm(a_2d, qweight.contiguous(), scales.contiguous(), qzeros.contiguous(),
-                          in_features=K, k_phys=K, group_rows=32, v1=True, bias=bias)
+    # The functional form has no load time: the tiled layout is written per
+    # call (one extra pass over the packed weight).
+    w = kernels.prepare(qweight.contiguous(), scales.contiguous(), qzeros.contiguous(), in_features=K,
+                        out_features=N, kmap=None, k_phys=K, group_rows=32, v1=True)
+    c = kernels.int4_gemm(a_2d, w, in_features=K, bias=bias)
     out = c.reshape(*leading_shape, N)
     if orig_dtype == torch.float32:
         out = out.to(torch.float32)

@@ -4,14 +4,14 @@ Constructor of the reference's ``PackedGPTQLinear``
 (layers/packed_gptq_linear.py:28-88). The reference dequantizes the whole
 weight to ``x.dtype`` on every call and then runs ``F.linear`` (:66-74); here
 4-bit layers run the fused HIP GEMM instead: act-order rows are sorted by
-group once at load time (``oc_int4_plan_groups`` + ``oc_int4_repack_rows``)
-and the kernel gathers the matching activation columns, so no weight is ever
+group once at load time (``oc_int4_plan_groups`` + ``oc_int4_prepare``)
+and the kernels read the matching activation columns, so no weight is ever
 materialised. The dequantized values are those of ``dequant_gptq_to_fp``
 (exact fp32 product, one rounding to the activation type); only the
 summation order differs.
 
 fp32 activations and 8-bit layers keep the reference's two-step evaluation,
-on the device: the HIP dequant kernel writes the dense weight in ``x.dtype``
+on the device: a HIP dequant kernel writes the dense weight in ``x.dtype``
 and ``F.linear`` multiplies it.
 """
 from __future__ import annotations
@@ -46,9 +46,7 @@ class PackedGPTQLinear(_HipGPTQLinear):
         if self.wbits == 4:
             self._setup(in_features, out_features, qweight, scales, qzeros, bias, groupsize,
                         g_idx, v1, "packed")
-            # Original-order copies for the two-step (fp32 activation) path.
             self.register_buffer("g_idx", g_idx.to(torch.long).contiguous())
-            self.register_buffer("qweight_orig", qweight.contiguous(), persistent=False)
         else:
             self.in_features = int(in_features)
             self.out_features = int(out_features)
@@ -59,26 +57,32 @@ class PackedGPTQLinear(_HipGPTQLinear):
             self.register_buffer("scales", scales.contiguous())
             self.register_buffer("qzeros", qzeros.contiguous())
             self.register_buffer("g_idx", g_idx.to(torch.long).contiguous())
-            self.qweight_orig = None
             if bias is not None:
                 self.register_buffer("bias", bias.contiguous())
             else:
                 self.bias = None
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.wbits == 4 and x.dtype in (torch.float16, torch.bfloat16):
-            return self._gemm(x)
-        qw = self.qweight_orig if self.wbits == 4 else self.qweight
-        weight = kernels.int4_dequant(qw, self.scales, self.qzeros, self.g_idx, self.in_features,
-                                      self.out_features, x.dtype, v1=self.v1, wbits=self.wbits)
+        if self.wbits == 4:
+            if x.dtype in (torch.float16, torch.bfloat16):
+                return self._gemm(x)
+            weight = self.dequantize(x.dtype)
+        else:
+            weight = kernels.int4_dequant(self.qweight, self.scales, self.qzeros, self.g_idx,
+                                          self.in_features, self.out_features, x.dtype, v1=self.v1,
+                                          wbits=self.wbits)
         bias = self.bias.to(x.dtype) if self.bias is not None else None
         return F.linear(x, weight, bias)
 
     def _apply(self, fn, recurse=True):
-        qw_orig = self.qweight_orig
-        result = super()._apply(fn, recurse=recurse)
-        if qw_orig is not None and self.qweight_orig.dtype != torch.int32:
-            self.qweight_orig = qw_orig.to(self.qweight_orig.device)
+        if self.wbits == 4:
+            return super()._apply(fn, recurse=recurse)
+        qw, qz = self.qweight, self.qzeros
+        result = torch.nn.Module._apply(self, fn, recurse=recurse)
+        if self.qweight.dtype != torch.int32:
+            self.qweight = qw.to(self.qweight.device)
+        if self.qzeros.dtype != torch.int32:
+            self.qzeros = qz.to(self.qzeros.device)
         return result
 
     def extra_repr(self) -> str:

@@ -113,21 +113,84 @@ def test_unpack_rows_matches_oracle(wbits):
     assert np.array_equal(z.cpu().numpy(), O.unpack_zeros(qz, wbits, 3 * (32 // wbits)))
 
 
-def test_repack_rows_matches_plan():
+def _untile(w, N):
+    """Tiled tensors -> physical packed rows [K_phys/8, N], scales [G, N], zeros [G, N]."""
+    qt, st, zt = w.qt.cpu().numpy(), w.st.cpu(), w.zt.cpu().numpy()
+    tiles, KS = qt.shape[:2]
+    packed = qt.transpose(1, 3, 0, 2).reshape(KS * 4, tiles * 16)[:, :N]
+    G = st.shape[1]
+    scales = st.permute(1, 0, 2).reshape(G, tiles * 16)[:, :N]
+    zw = zt.view(np.uint32)  # [tiles, G, 2]
+    nib = (zw[..., None] >> (4 * np.arange(8, dtype=np.uint32))) & 15  # [tiles, G, 2, 8]
+    zeros = nib.reshape(tiles, G, 16).transpose(1, 0, 2).reshape(G, tiles * 16)[:, :N]
+    return packed, scales, zeros.astype(np.int32)
+
+
+def test_prepare_layout_odd_groups():
+    """gs 26: the physical rows of the tiled layout are the reference's
+    ``_repack_groups_to_32`` output; scales copied, v1 zeros restored (+1)."""
     from onecomp_runtime import kernels, synthetic
 
-    K, N = 1040, 64
+    K, N = 1040, 72  # 5 tiles, the last one half full
     layer = synthetic.gptq_layer(K, N, seed=7, groupsize=26)
     plan = kernels.plan_groups(K, 26)
-    say("repack rows gs=26")
-    out = kernels.repack_rows(layer.qweight.to(DEV), K, torch.from_numpy(plan.kmap).to(DEV), plan.k_phys)
-    codes = O.unpack_rows(out.cpu().numpy(), plan.k_phys, 4)
-    want = np.zeros((plan.k_phys, N), np.int32)
-    live = plan.kmap >= 0
-    want[live] = layer.codes.numpy()[plan.kmap[live]]
-    assert np.array_equal(codes, want)
+    say("prepare layout gs=26")
+    w = kernels.prepare(layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV), in_features=K,
+                        out_features=N, kmap=torch.from_numpy(plan.kmap).to(DEV), k_phys=plan.k_phys,
+                        group_rows=plan.group_rows, v1=True)
+    assert w.qt.shape == (5, plan.k_phys // 32, 16, 4) and w.zt.shape == (5, K // 26, 2)
+    packed, scales, zeros = _untile(w, N)
     ref_pad, kp = O.repack_groups_to_32(layer.qweight.numpy(), K, N, 26)
-    assert kp == plan.k_phys and np.array_equal(out.cpu().numpy(), ref_pad)
+    assert kp == plan.k_phys and np.array_equal(packed, ref_pad)
+    assert torch.equal(scales, layer.scales)
+    assert np.array_equal(zeros, (O.unpack_zeros(layer.qzeros.numpy(), 4, N) + 1) & 15)
+    # columns beyond N in the last tile are zero
+    assert not w.qt[-1, :, 8:].any() and not w.st[-1, :, 8:].any() and not w.zt[-1, :, 1].any()
+
+
+def test_prepare_layout_act_order_v2():
+    """act-order: physical row r holds input row kmap[r] (rows sorted by group)."""
+    from onecomp_runtime import kernels, synthetic
+
+    K, N = 1024, 48
+    layer = synthetic.gptq_layer(K, N, seed=9, groupsize=128, v1=False, act_order=True)
+    plan = kernels.plan_groups(K, 128, layer.g_idx)
+    say("prepare layout act-order v2")
+    w = kernels.prepare(layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV), in_features=K,
+                        out_features=N, kmap=torch.from_numpy(plan.kmap).to(DEV), k_phys=plan.k_phys,
+                        group_rows=plan.group_rows, v1=False)
+    packed, scales, zeros = _untile(w, N)
+    assert np.array_equal(O.unpack_rows(packed, K, 4), layer.codes.numpy()[plan.kmap])
+    assert torch.equal(scales, layer.scales)
+    assert np.array_equal(zeros, O.unpack_zeros(layer.qzeros.numpy(), 4, N))
+
+
+@pytest.mark.parametrize("K,N,gs,v1,act,out_dtype,scale_dtype", [
+    (1040, 72, 26, True, False, torch.bfloat16, torch.float16),     # odd groups, ragged tile
+    (5120, 1024, 32, True, True, torch.bfloat16, torch.float16),    # act-order gs 32
+    (1024, 256, 128, False, True, torch.float16, torch.bfloat16),   # act-order gs 128, v2
+    (1000, 40, 32, True, False, torch.float32, torch.float16),      # ragged K and N
+    (4096, 512, 32, True, False, torch.float16, torch.float16),
+])
+def test_dequant_tiled_bit_exact(K, N, gs, v1, act, out_dtype, scale_dtype):
+    """prepare -> dequant_tiled reproduces dequant_gptq_to_fp bit for bit."""
+    from onecomp_runtime import kernels, synthetic
+
+    say(f"dequant tiled K={K} N={N} gs={gs} v1={v1} act={act} out={out_dtype} scales={scale_dtype}")
+    layer = synthetic.gptq_layer(K, N, seed=13, groupsize=gs, v1=v1, act_order=act, scale_dtype=scale_dtype)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    ref = O.dequant_gptq(qw, sc, qz, g_idx, K, N, {torch.bfloat16: "bf16", torch.float16: "f16",
+                                                   torch.float32: "f32"}[out_dtype], v1)
+    plan = kernels.plan_groups(K, gs, layer.g_idx if act else None)
+    kmap = None if plan.identity else torch.from_numpy(plan.kmap).to(DEV)
+    w = kernels.prepare(layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV), in_features=K,
+                        out_features=N, kmap=kmap, k_phys=plan.k_phys, group_rows=plan.group_rows, v1=v1)
+    out = kernels.dequant_tiled(w, kmap, K, out_dtype)
+    assert out.shape == (N, K)
+    if out_dtype == torch.float32:
+        assert np.array_equal(out.cpu().numpy().view(np.uint32), ref.view(np.uint32))
+    else:
+        assert np.array_equal(bits16(out), oracle_bits(ref, out_dtype))
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16, torch.float32])

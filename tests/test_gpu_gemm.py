@@ -15,7 +15,7 @@ from oracle import onecomp_oracle as O
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
-SPLITK, TILED, AUTO = 1, 2, 0
+SPLITK, TILED, AUTO, DOT = 1, 2, 0, 3
 
 
 def _module_for(layer, dtype=torch.bfloat16):
@@ -42,9 +42,8 @@ def _oracle_out(layer, x: torch.Tensor, dtype="bf16", bias=None):
 def _gemm_raw(mod, x, regime):
     from onecomp_runtime import kernels
 
-    return kernels.int4_gemm(x, mod.qweight, mod.scales, mod.qzeros, in_features=mod.in_features,
-                             k_phys=mod.k_phys, group_rows=mod.group_rows, v1=mod.v1, kmap=mod.kmap,
-                             bias=mod.bias, regime=regime)
+    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, bias=mod.bias,
+                             regime=regime)
 
 
 # -- benchmark workloads ------------------------------------------------------
@@ -218,23 +217,20 @@ def test_3d_and_noncontiguous_input():
     assert_gemm_close(mod(wide.to(DEV)[:, ::2]), _oracle_out(layer, x), "strided")
 
 
-@pytest.mark.parametrize("regime", [SPLITK, TILED])
-def test_deterministic_and_workspace_self_cleaning(regime):
-    from onecomp_runtime import _hip, synthetic
+@pytest.mark.parametrize("regime,M", [(DOT, 1), (DOT, 2), (SPLITK, 8), (TILED, 128), (TILED, 300)])
+def test_deterministic(regime, M):
+    """Fixed reduction orders (wave tree, split-K partials in split order)."""
+    from onecomp_runtime import synthetic
 
-    K, N, M = 8192, 1024, 8 if regime == SPLITK else 128
+    K, N = 8192, 1024
     layer = synthetic.gptq_layer(K, N, seed=59)
     mod = _module_for(layer)
     x = synthetic.activations(M, K, seed=60).to(DEV)
-    say(f"determinism regime={regime}")
+    say(f"determinism regime={regime} M={M}")
     a = _gemm_raw(mod, x, regime)
     b = _gemm_raw(mod, x, regime)
     assert torch.equal(a.view(torch.int16), b.view(torch.int16))
-    nbytes = int(_hip.lib().oc_int4_gemm_workspace_bytes(M, N, mod.k_phys, regime))
-    if nbytes:
-        ws = _hip.workspace.get(x.device, nbytes)
-        tiles = 16  # at least this many tile counters sit at the front of the workspace
-        assert int(ws[: 4 * tiles].view(torch.int32).abs().sum().item()) == 0
+    assert_gemm_close(a, _oracle_out(layer, x.cpu()), "determinism")
 
 
 def test_abi_rejects_bad_arguments():
@@ -244,13 +240,111 @@ def test_abi_rejects_bad_arguments():
     qw, sc, qz = layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV)
     x = synthetic.activations(4, 256, seed=62).to(DEV)
     say("ABI argument errors")
+    w = kernels.prepare(qw, sc, qz, in_features=256, out_features=64, kmap=None, k_phys=256, group_rows=32,
+                        v1=True)
     with pytest.raises(ValueError):  # K_phys not a multiple of 32
-        kernels.int4_gemm(x, qw, sc, qz, in_features=256, k_phys=250, group_rows=32, v1=True)
+        kernels.int4_gemm(x, kernels.TiledWeights(w.qt, w.st, w.zt, 64, 250, 32), in_features=256)
     with pytest.raises(ValueError):  # N not a multiple of 8
-        kernels.int4_gemm(x, qw[:, :60], sc[:, :60], qz, in_features=256, k_phys=256, group_rows=32,
-                          v1=True)
+        kernels.int4_gemm(x, kernels.TiledWeights(w.qt, w.st, w.zt, 60, 256, 32), in_features=256)
+    with pytest.raises(ValueError):  # the layout needs N % 8 == 0 as well
+        kernels.prepare(qw[:, :60].contiguous(), sc[:, :60].contiguous(), qz, in_features=256, out_features=60,
+                        kmap=None, k_phys=256, group_rows=32, v1=True)
+    with pytest.raises(ValueError):  # group_rows must divide K_phys
+        kernels.prepare(qw, sc, qz, in_features=256, out_features=64, kmap=None, k_phys=256, group_rows=96,
+                        v1=True)
     with pytest.raises(NotImplementedError):  # split-K regime is for M <= 64
-        kernels.int4_gemm(torch.zeros((65, 256), dtype=torch.bfloat16, device=DEV), qw, sc, qz,
-                          in_features=256, k_phys=256, group_rows=32, v1=True, regime=SPLITK)
+        kernels.int4_gemm(torch.zeros((65, 256), dtype=torch.bfloat16, device=DEV), w, in_features=256,
+                          regime=SPLITK)
+    with pytest.raises(NotImplementedError):  # decode regime is for M <= 2
+        kernels.int4_gemm(x, w, in_features=256, regime=DOT)
     with pytest.raises(RuntimeError):  # host tensors are refused
-        kernels.int4_gemm(x.cpu(), qw, sc, qz, in_features=256, k_phys=256, group_rows=32, v1=True)
+        kernels.int4_gemm(x.cpu(), w, in_features=256)
+
+
+@pytest.mark.parametrize("M", [1, 8, 200])
+def test_graph_capture_replays_match_eager(M):
+    """Captured launches (split-K counters and workspace included) replay
+    correctly several times, with eager work in between."""
+    from onecomp_runtime import synthetic
+
+    K, N = 4096, 1024
+    layer = synthetic.gptq_layer(K, N, seed=63, act_order=(M == 1))
+    mod = _module_for(layer)
+    x = synthetic.activations(M, K, seed=64).to(DEV)
+    say(f"graph capture M={M}")
+    with torch.no_grad():
+        eager = mod(x).clone()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = mod(x)
+        for rep in range(4):
+            g.replay()
+            other = mod(synthetic.activations(M, K, seed=65 + rep).to(DEV))  # eager work in between
+            torch.cuda.synchronize()
+            assert torch.equal(out.view(torch.int16), eager.view(torch.int16)), f"replay {rep}"
+            del other
+
+
+@pytest.mark.parametrize("kind", ["gs32_v1", "v2", "actorder", "gs26", "gs128", "fp16", "bf16_scales"])
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_kernel_one_hot_bit_exact(kind, M):
+    """The decode (dot2, factored-scale) kernel reproduces dequantized rows exactly."""
+    from onecomp_runtime import synthetic
+
+    K, N = 1024, 320
+    kw = dict(seed=71)
+    dtype = torch.float16 if kind == "fp16" else torch.bfloat16
+    if kind == "v2":
+        kw["v1"] = False
+    if kind == "actorder":
+        kw["act_order"] = True
+    if kind == "gs26":
+        K, kw["groupsize"] = 1040, 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    if kind == "bf16_scales":
+        kw["scale_dtype"] = torch.bfloat16
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer, dtype)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16" if dtype == torch.bfloat16 else "f16", layer.v1)
+    rng = np.random.default_rng(1)
+    for rep in range(3):
+        ks = rng.choice(K, M, replace=False)
+        x = torch.zeros((M, K), dtype=dtype)
+        x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+        say(f"decode one-hot kind={kind} M={M} rep={rep}")
+        out = _gemm_raw(mod, x.to(DEV), DOT)
+        assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
+
+
+@pytest.mark.parametrize("K,N", [(32, 8), (1000, 200), (5120, 1024), (4096, 4096), (2048, 17408)])
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("act", [False, True])
+def test_decode_kernel_matches_oracle(K, N, M, act):
+    from onecomp_runtime import synthetic
+
+    layer = synthetic.gptq_layer(K, N, seed=72 + K, act_order=act)
+    x = synthetic.activations(M, K, seed=73)
+    mod = _module_for(layer)
+    say(f"decode kernel K={K} N={N} M={M} act={act}")
+    assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"dot {K}x{N} M={M}")
+    assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), "auto")
+
+
+@pytest.mark.parametrize("regime", [DOT, SPLITK, TILED])
+@pytest.mark.parametrize("M", [1, 2])
+def test_small_m_bias_all_regimes(regime, M):
+    """Bias epilogue and act-order on every regime that takes a decode batch."""
+    from onecomp_runtime import synthetic
+    from onecomp_runtime.layers import PackedGPTQLinear
+
+    K, N = 2048, 1536
+    layer = synthetic.gptq_layer(K, N, seed=74, act_order=True)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    mod = PackedGPTQLinear(K, N, layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV),
+                           g_idx=layer.g_idx.to(DEV), bias=bias.to(DEV), groupsize=32)
+    x = synthetic.activations(M, K, seed=75)
+    say(f"small-M bias regime={regime} M={M}")
+    assert_gemm_close(_gemm_raw(mod, x.to(DEV), regime), _oracle_out(layer, x, bias=bias.float()),
+                      f"regime {regime} M={M}")

@@ -147,8 +147,8 @@ def test_moe_grouped_gemm(E, K, N, T, topk):
     x = synthetic.activations(T, K, seed=20331)
     ids = synthetic.router_topk(T, E, topk, seed=20332)
     off, pairs = kernels.moe_route(ids.to(DEV), E)
-    y = kernels.int4_moe_gemm(x.to(DEV), topk, experts.qweight.to(DEV), experts.scales.to(DEV),
-                              experts.qzeros.to(DEV), off, pairs)
+    w = kernels.prepare_experts(experts.qweight.to(DEV), experts.scales.to(DEV), experts.qzeros.to(DEV))
+    y = kernels.int4_moe_gemm(x.to(DEV), topk, w, off, pairs)
     assert y.shape == (T * topk, N)
     used = np.unique(ids.numpy())
     ws = {}
@@ -251,12 +251,35 @@ def test_module_dtype_moves_keep_packed_buffers():
                                       layer.qzeros.to(DEV), groupsize=26)
     say("module .to(dtype)")
     mod = mod.to(torch.float32)
-    assert mod.qweight.dtype == torch.int32 and mod.qzeros.dtype == torch.int32
-    assert mod.kmap.dtype == torch.int32 and mod.scales.dtype == torch.float16
+    assert mod.qweight_tiled.dtype == torch.int32 and mod.zeros_tiled.dtype == torch.int32
+    assert mod.kmap.dtype == torch.int32 and mod.scales_tiled.dtype == torch.float16
     mod.warmup((1, 40))
     x = synthetic.activations(3, 104, seed=93)
     assert_gemm_close(mod(x.to(DEV)), O.gptq_linear(np32(x), *layer_oracle_inputs(layer), 104, 64, "bf16"),
                       "after .to")
+
+
+def test_layer_built_on_host_prepares_on_first_device_forward():
+    """A layer constructed from CPU tensors (the reference allows it) keeps the
+    checkpoint tensors until it is moved; the first device forward tiles them."""
+    from onecomp_runtime import synthetic
+    from onecomp_runtime.layers import PackedGPTQLinear
+
+    layer = synthetic.gptq_layer(512, 96, seed=94, act_order=True, v1=False)
+    mod = PackedGPTQLinear(512, 96, layer.qweight, layer.scales, layer.qzeros, g_idx=layer.g_idx,
+                           groupsize=32, v1=False)
+    assert mod.qweight_tiled is None
+    with pytest.raises(RuntimeError):
+        mod.tiled()
+    mod = mod.to(DEV)
+    x = synthetic.activations(5, 512, seed=95)
+    say("host-built layer, first device forward")
+    out = mod(x.to(DEV))
+    assert mod.qweight_tiled is not None and mod._src_qweight is None
+    assert_gemm_close(out, O.gptq_linear(np32(x), *layer_oracle_inputs(layer), 512, 96, "bf16", False),
+                      "host-built")
+    wd = O.dequant_gptq(*layer_oracle_inputs(layer), 512, 96, "f16", False)
+    assert np.array_equal(bits16(mod.dequantize(torch.float16)), oracle_bits(wd, torch.float16))
 
 
 class _TinyBlock(torch.nn.Module):

@@ -153,10 +153,13 @@ def test_modules_refuse_host_tensors_without_fallback():
         FusedInt4LinearPaddedGroups(64, 16, torch.from_numpy(layer),
                                     torch.ones(2, 16, dtype=torch.float16),
                                     torch.zeros(2, 2, dtype=torch.int32), groupsize=32)
-    with pytest.raises(ValueError):  # odd groups are re-laid on the device only
-        FusedInt4LinearPaddedGroups(52, 16, torch.from_numpy(O.pack_rows(np.zeros((52, 16)))),
-                                    torch.ones(2, 16, dtype=torch.float16),
-                                    torch.zeros(2, 2, dtype=torch.int32), groupsize=26)
+    # host-built layers keep the checkpoint tensors; the layout is written on the device
+    padded = FusedInt4LinearPaddedGroups(52, 16, torch.from_numpy(O.pack_rows(np.zeros((52, 16)))),
+                                         torch.ones(2, 16, dtype=torch.float16),
+                                         torch.zeros(2, 2, dtype=torch.int32), groupsize=26)
+    assert padded.qweight_tiled is None and padded.padded_in_features == 64
+    with pytest.raises(RuntimeError, match="HIP device"):
+        padded(torch.zeros(1, 52, dtype=torch.bfloat16))
 
 
 def test_loader_rejects_checkpoint_without_metadata(tmp_path):
