@@ -166,6 +166,10 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  *            aligned), a_dtype in {F16, BF16}
  *   qt/st/zt tiled weights from oc_int4_prepare (scale_dtype F16 or BF16)
  *   kmap     NULL or int32 [K_phys] (device, 16-byte aligned)
+ *   kinv     NULL or uint16 [K_logical] (device, 16-byte aligned), the
+ *            inverse of kmap: kinv[kmap[k']] = k'. The decode regime stages
+ *            activations through it and needs it whenever kmap is given
+ *            (OC_REGIME_AUTO picks another regime without it).
  *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
  *   c        [M, N] (row stride ldc elements) of a_dtype
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
@@ -179,7 +183,8 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
                  int32_t K_logical, const int32_t *qt, const void *st,
                  int32_t scale_dtype, const int32_t *zt, int32_t N,
                  int32_t K_phys, int32_t group_rows, const int32_t *kmap,
-                 const void *bias, int32_t bias_dtype, void *c, int64_t ldc,
+                 const uint16_t *kinv, const void *bias, int32_t bias_dtype,
+                 void *c, int64_t ldc,
                  void *workspace, size_t workspace_bytes, int32_t regime,
                  void *stream);
 

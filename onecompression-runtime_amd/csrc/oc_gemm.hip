@@ -45,7 +45,7 @@ struct GemmParams {
   int G;               // K_phys / group_rows
   int group_rows;
   int gshift;          // log2(group_rows / 32), or -1
-  const int32_t *kmap;  // decode kernel only (the MFMA regimes get gathered activations)
+  const uint16_t *kinv;  // decode regime: logical -> physical row (NULL: identity)
   const void *bias;
   int bias_dtype;
   void *c;
@@ -88,19 +88,33 @@ __device__ __forceinline__ int xcd_block(int bid, int nblocks) {
 }
 
 // ---------------------------------------------------------------------------
-// Decode kernel (M <= 2). grid = tiles, 256 threads. Lane (c = l%16, h = l/16)
-// of wave w owns column 16t + c and the K steps lp, lp+16, ... (lp = 4w + h),
-// so each wave instruction reads four consecutive K steps of the tile (1 KB).
+// Decode kernel (M <= 2). grid = tiles, 64*WAVES threads. Lane (c = l%16,
+// h = l/16) of wave w owns column 16t + c and the K steps lp, lp + NPH, ...
+// (lp = 4w + h, NPH = 4*WAVES phases), so each wave instruction reads four
+// consecutive K steps of the tile (1 KB).
 //
 // The scale and zero are factored out of each 32-row group:
 //   sum_k x_k * s * (w_k - z) = s * (sum_k x_k * (B + w_k) - (B + z) * sum_k x_k)
 // where B + w_k is the exact 16-bit number made by OR-ing the 4-bit code into
 // the mantissa of B (bf16 128.0 / fp16 1024.0). The first sum runs on
-// v_dot2_f32_{bf16,f16} (fp32 accumulation) against activation pairs staged
-// once per workgroup in LDS (permuted by kmap, interleaved to match the code
-// pairs (i, i+4) of a packed word), the second from per-step activation sums
-// staged beside them.
-constexpr int DOT_PF = 8;
+// v_dot2_f32_{bf16,f16} (fp32 accumulation) against activation pairs held in
+// LDS, interleaved to match the code pairs (i, i+4) of a packed word; the
+// second uses per-step activation sums staged beside them.
+//
+// Activation staging ("x-pairs", in LDS): for row m and K step ks, 4 uint4
+// of pairs (one per 8-row octet w: {x0|x4<<16, x1|x5<<16, x2|x6<<16,
+// x3|x7<<16}) and a float2 (sum, B * sum): pairs [MR][KS][4] uint4, then sums
+// [MR][KSP] float2 (KSP = KS rounded up to even).
+//
+// Act-order / padded layers read their activation rows contiguously and
+// scatter each value to its physical row through kinv (logical -> physical),
+// so every global access of the staging stays coalesced; a per-workgroup
+// gather through kmap would touch one cache line per lane.
+constexpr int DOT_PF = 3;  // K steps in flight per lane
+
+// How the decode kernel stages its activations: contiguous rows, or rows
+// scattered to their physical positions through kinv (act-order / padded).
+enum { XS_CONTIG = 0, XS_SCATTER = 1 };
 
 template <int DT>
 __device__ __forceinline__ float dot2acc(uint32_t b, uint32_t x, float acc) {
@@ -117,23 +131,66 @@ __device__ __forceinline__ float half_to_f32(uint32_t h16) {
   else return f16_to_f32(static_cast<uint16_t>(h16));
 }
 
-size_t dot_lds_bytes(int MR, int KS) {
-  return static_cast<size_t>(MR) * KS * (4 * sizeof(uint4) + sizeof(float2));
+template <int DT>
+constexpr float dot_base() {
+  return DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
 }
 
-template <int DT, int SDT, int MR, bool KMAP>
-__global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
+// Pair words of one octet given as 4 raw words {x0|x1<<16, x2|x3<<16, ...},
+// and the octet's sum (fp32, in row order).
+template <int DT>
+__device__ __forceinline__ uint4 octet_pairs(uint4 raw, float &sum) {
+  const uint32_t lo = 0x05040100u, hi = 0x07060302u;  // v_perm selectors: low / high halves of two words
+  uint4 r;
+  r.x = __builtin_amdgcn_perm(raw.z, raw.x, lo);  // x0 | x4 << 16
+  r.y = __builtin_amdgcn_perm(raw.z, raw.x, hi);  // x1 | x5 << 16
+  r.z = __builtin_amdgcn_perm(raw.w, raw.y, lo);  // x2 | x6 << 16
+  r.w = __builtin_amdgcn_perm(raw.w, raw.y, hi);  // x3 | x7 << 16
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += half_to_f32<DT>(w[i] & 0xFFFFu);
+    s += half_to_f32<DT>(w[i] >> 16);
+  }
+  sum = s;
+  return r;
+}
+
+__host__ __device__ inline int dot_ksp(int KS) { return (KS + 1) & ~1; }
+size_t dot_lds_bytes(int MR, int KS) {
+  return static_cast<size_t>(MR) * (KS * 4 * sizeof(uint4) + dot_ksp(KS) * sizeof(float2));
+}
+
+// Physical row r of activation row m -> its 16-bit slot in the x-pair block.
+__device__ __forceinline__ int xpair_slot(int m, int K_phys, int r) {
+  return m * K_phys + (r & ~7) + ((r & 3) << 1) + ((r >> 2) & 1);
+}
+
+template <int DT, int SDT, int MR, int XS, int WAVES, int TPW>
+__global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
+  // 16-byte activation words staged per thread per round trip (registers
+  // beyond the main loop's would cost occupancy).
+  constexpr int SB = XS == XS_CONTIG ? 4 : 2;
+  constexpr int NT = 64 * WAVES;
+  constexpr int WPT = WAVES / TPW;  // waves per tile
+  constexpr int NPH = 4 * WPT;      // K-step phases per tile
   constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
-  constexpr float BASE = DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
   extern __shared__ __attribute__((aligned(16))) uint4 dot_lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int c = lane & 15, h = lane >> 4;
-  const int lp = 4 * wave + h;
-  const int t = xcd_block(blockIdx.x, gridDim.x);
+  const int lp = 4 * (wave % WPT) + h;
+  // TPW tiles per workgroup share one activation staging.
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+  const int tw = xcd_block(blockIdx.x, gridDim.x) * TPW + wave / WPT;
+  const bool live = tw < tiles;  // the last workgroup may have fewer tiles
+  const int t = live ? tw : tiles - 1;
   const int n = TILE_N * t + c;
   const int KS = p.KS, M = p.M;
+  const int ks_end = live ? KS : 0;
+  const int KSP = (KS + 1) & ~1;
   uint4 *xpairs = dot_lds;                                          // [MR][KS * 4]
-  float2 *xsum = reinterpret_cast<float2 *>(dot_lds + MR * KS * 4);  // [MR][KS]: (sum, BASE * sum)
+  float2 *xsum = reinterpret_cast<float2 *>(dot_lds + MR * KS * 4);  // [MR][KSP]: (sum, B * sum)
   const uint4 *qt4 = static_cast<const uint4 *>(p.qw) + static_cast<int64_t>(t) * KS * TILE_N + c;
   const uint16_t *stp = static_cast<const uint16_t *>(p.scales) + static_cast<int64_t>(t) * p.G * TILE_N + c;
   const uint32_t *ztp = static_cast<const uint32_t *>(p.zeros) + static_cast<int64_t>(t) * p.G * 2 + (c >> 3);
@@ -150,56 +207,101 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
     S.s = stp[g * TILE_N];
     S.z = ztp[g * 2];
   };
+  // The head of the weight stream is in flight while activations stage.
 #pragma unroll
   for (int f = 0; f < DOT_PF; ++f) {
-    const int ks = lp + 16 * f;
-    if (ks < KS) load(st[f], ks);
+    const int ks = lp + NPH * f;
+    if (ks < ks_end) load(st[f], ks);
   }
 
-  // Stage activations: one thread per K step and row.
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
+  if constexpr (XS == XS_CONTIG) {
+    // One thread per octet (8 physical rows = 8 logical rows); the 4 octets
+    // of a K step sit in 4 consecutive lanes, which add up the step's sum.
+    const int per_row = KS * 4;
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    if (m >= M) break;
-    const uint16_t *arow = a + static_cast<int64_t>(m) * p.lda;
-    for (int ks = tid; ks < KS; ks += blockDim.x) {
-      uint32_t v[32];
-      if constexpr (KMAP) {
-        int src[32];
+    for (int m = 0; m < MR; ++m) {
+      const uint4 *arow = reinterpret_cast<const uint4 *>(a + static_cast<int64_t>(m) * p.lda);
+      for (int base = 0; base < per_row; base += NT * SB) {
+        uint4 raw[SB];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const int4 k4 = *reinterpret_cast<const int4 *>(p.kmap + 32 * ks + 4 * i);
-          src[4 * i] = k4.x; src[4 * i + 1] = k4.y; src[4 * i + 2] = k4.z; src[4 * i + 3] = k4.w;
-        }
-        // Rows without a source (-1, or anything outside [0, K_logical)) read as zero.
-        uint32_t g[32];
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          if (static_cast<unsigned>(src[i]) >= static_cast<unsigned>(p.K_logical)) src[i] = -1;
-          g[i] = arow[max(src[i], 0)];
+        for (int u = 0; u < SB; ++u) {
+          const int i = base + NT * u + tid;
+          raw[u] = i < per_row ? arow[i] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
-        for (int i = 0; i < 32; ++i) v[i] = src[i] >= 0 ? g[i] : 0u;
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint4 raw = *reinterpret_cast<const uint4 *>(arow + 32 * ks + 8 * i);
-          v[8 * i + 0] = raw.x & 0xFFFFu; v[8 * i + 1] = raw.x >> 16;
-          v[8 * i + 2] = raw.y & 0xFFFFu; v[8 * i + 3] = raw.y >> 16;
-          v[8 * i + 4] = raw.z & 0xFFFFu; v[8 * i + 5] = raw.z >> 16;
-          v[8 * i + 6] = raw.w & 0xFFFFu; v[8 * i + 7] = raw.w >> 16;
+        for (int u = 0; u < SB; ++u) {
+          const int i = base + NT * u + tid;
+          float sum;
+          const uint4 pr = octet_pairs<DT>(raw[u], sum);
+          sum += __shfl_xor(sum, 1);
+          sum += __shfl_xor(sum, 2);
+          if (i < per_row) {
+            xpairs[m * per_row + i] = pr;
+            if ((i & 3) == 0) xsum[m * KSP + (i >> 2)] = make_float2(sum, dot_base<DT>() * sum);
+          }
         }
       }
+    }
+  } else {
+    uint16_t *x16 = reinterpret_cast<uint16_t *>(xpairs);
+    const int K = p.K_logical, K_phys = p.K_phys;
+    if (K != K_phys) {  // physical rows without a source stay zero
+      for (int i = tid; i < MR * KS * 4; i += NT) xpairs[i] = make_uint4(0, 0, 0, 0);
+      __syncthreads();
+    }
+    // Logical octets: 8 activations and their 8 physical rows (one 16-byte
+    // load each); the K % 8 tail rows one by one.
+    const int octets = K >> 3;
+    const uint4 *kinv4 = reinterpret_cast<const uint4 *>(p.kinv);
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const uint16_t *arow = a + static_cast<int64_t>(m) * p.lda;
+      for (int base = 0; base < octets; base += NT * SB) {
+        uint4 xv[SB], rv[SB];
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int i = base + NT * u + tid;
+          if (i < octets) {
+            xv[u] = reinterpret_cast<const uint4 *>(arow)[i];
+            rv[u] = kinv4[i];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < SB; ++u) {
+          const int i = base + NT * u + tid;
+          if (i < octets) {
+            const uint32_t xw[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+            const uint32_t rw[4] = {rv[u].x, rv[u].y, rv[u].z, rv[u].w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r0 = static_cast<int>(rw[j] & 0xFFFFu), r1 = static_cast<int>(rw[j] >> 16);
+              if (r0 < K_phys) x16[xpair_slot(m, K_phys, r0)] = static_cast<uint16_t>(xw[j]);
+              if (r1 < K_phys) x16[xpair_slot(m, K_phys, r1)] = static_cast<uint16_t>(xw[j] >> 16);
+            }
+          }
+        }
+      }
+      for (int k = 8 * octets + tid; k < K; k += NT) {
+        const int r = p.kinv[k];
+        if (r < K_phys) x16[xpair_slot(m, K_phys, r)] = arow[k];
+      }
+    }
+    __syncthreads();
+    // Step sums from the staged pairs (dot2 against 1.0 pairs).
+    const uint32_t ones = DT == OC_DTYPE_BF16 ? 0x3F803F80u : 0x3C003C00u;
+    for (int i = tid; i < MR * KS; i += NT) {
       float sum = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint32_t *o = v + 8 * w;
-        xpairs[(m * KS + ks) * 4 + w] =
-            make_uint4(o[0] | (o[4] << 16), o[1] | (o[5] << 16), o[2] | (o[6] << 16), o[3] | (o[7] << 16));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) sum += half_to_f32<DT>(o[i]);
+        const uint4 pr = xpairs[4 * i + w];
+        sum = dot2acc<DT>(pr.x, ones, sum);
+        sum = dot2acc<DT>(pr.y, ones, sum);
+        sum = dot2acc<DT>(pr.z, ones, sum);
+        sum = dot2acc<DT>(pr.w, ones, sum);
       }
-      xsum[m * KS + ks] = make_float2(sum, BASE * sum);
+      const int m = i / KS, ks = i - m * KS;
+      xsum[m * KSP + ks] = make_float2(sum, dot_base<DT>() * sum);
     }
   }
   __syncthreads();
@@ -208,13 +310,13 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = 0.f;
   const uint32_t magic = MAGIC;
-  for (int base = lp; base < KS; base += 16 * DOT_PF) {
+  for (int base = lp; base < ks_end; base += NPH * DOT_PF) {
 #pragma unroll
     for (int f = 0; f < DOT_PF; ++f) {
-      const int ks = base + 16 * f;
-      if (ks >= KS) break;
+      const int ks = base + NPH * f;
+      if (ks >= ks_end) break;
       const Stage cur = st[f];
-      if (ks + 16 * DOT_PF < KS) load(st[f], ks + 16 * DOT_PF);
+      if (ks + NPH * DOT_PF < ks_end) load(st[f], ks + NPH * DOT_PF);
       float d[MR];
 #pragma unroll
       for (int m = 0; m < MR; ++m) d[m] = 0.f;
@@ -239,13 +341,13 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
       const float s = scale_f32<SDT>(cur.s);
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
-        const float2 xs = xsum[m * KS + ks];
+        const float2 xs = xsum[m * KSP + ks];
         acc[m] = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, d[m] - xs.y), acc[m]);
       }
     }
   }
 
-  // Phases h of one wave (xor 16, 32), then the 4 waves through LDS in order.
+  // Phases h of one wave (xor 16, 32), then the waves through LDS in order.
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     acc[m] += __shfl_xor(acc[m], 16);
@@ -258,12 +360,14 @@ __global__ __launch_bounds__(256) void gemv_dot_kernel(GemmParams p) {
     for (int m = 0; m < MR; ++m) red[wave][m][c] = acc[m];
   }
   __syncthreads();
-  if (wave != 0 || h != 0 || n >= p.N) return;
+  if (wave % WPT != 0 || h != 0 || !live || n >= p.N) return;
   const float bv = bias_at(p, n);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m >= M) break;
-    const float v = ((red[0][m][c] + red[1][m][c]) + red[2][m][c]) + red[3][m][c];
+    float v = red[wave][m][c];
+#pragma unroll
+    for (int w = 1; w < WPT; ++w) v += red[wave + w][m][c];
     store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bv);
   }
 }
@@ -669,6 +773,9 @@ int ilog2_exact(int v) {
 
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
+// Decode launch shapes: waves per workgroup x tiles per workgroup.
+enum { DOT_W8_T1 = 0, DOT_W8_T2 = 1, DOT_W4_T1 = 2 };
+
 struct Plan {
   int regime;
   int mt;        // small-M kernel: row tiles of 16
@@ -676,6 +783,7 @@ struct Plan {
   int ksplit;
   int ksteps_per_split;
   bool gather;   // activations gathered into physical order first (kmap, MFMA regimes)
+  int waves;     // decode kernel: launch shape (DOT_W*_T*)
 };
 
 // The decode kernel takes M <= 2, power-of-two groups of 32-row steps and its
@@ -684,21 +792,27 @@ bool dot_eligible(int M, int K_phys, int group_rows) {
   return M >= 1 && M <= 2 && ilog2_exact(group_rows / 32) >= 0 && dot_lds_bytes(M, K_phys / 32) <= 128 * 1024;
 }
 
-Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime) {
+Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime, bool has_kinv = true) {
   Plan sp{};
   const int ksteps = K_phys / 32;
   // Tuning knobs, read once per process.
   static const bool dot_disabled = env_int("ONECOMP_HIP_DISABLE_DOT", 0) != 0;
   static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
   if (regime == OC_REGIME_AUTO) {
-    if (!dot_disabled && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
+    if (!dot_disabled && (!has_kmap || has_kinv) && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
     else regime = M <= 64 ? OC_REGIME_SPLITK : OC_REGIME_TILED;
   }
   sp.regime = regime;
   sp.ksplit = 1;
   sp.ksteps_per_split = ksteps;
   sp.gather = has_kmap && regime != OC_REGIME_DOT;
-  if (regime == OC_REGIME_DOT) return sp;
+  if (regime == OC_REGIME_DOT) {
+    static const int dot_shape = env_int("ONECOMP_HIP_DOT_SHAPE", -1);
+    // Measured best on MI355X for 1024 <= N <= 17408: 8 waves, one tile per
+    // workgroup. ONECOMP_HIP_DOT_SHAPE overrides (tuning only).
+    sp.waves = dot_shape >= DOT_W8_T1 && dot_shape <= DOT_W4_T1 ? dot_shape : DOT_W8_T1;
+    return sp;
+  }
   if (regime == OC_REGIME_SPLITK) {
     sp.mt = std::max(1, (M + 15) / 16);
     return sp;
@@ -722,7 +836,7 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   return sp;
 }
 
-// Workspace: [gathered activations (bf16/fp16, M x K_phys)][split-K partials].
+// Workspace: [gathered activations (M x K_phys 16-bit)][split-K partials].
 size_t gather_bytes(const Plan &sp, int M, int K_phys) {
   return sp.gather ? align256(static_cast<size_t>(M) * K_phys * 2) : 0;
 }
@@ -732,24 +846,36 @@ size_t workspace_bytes(const Plan &sp, int M, int N, int K_phys) {
   return b;
 }
 
-template <int DT, int SDT, int MR, bool KMAP>
+template <int DT, int SDT, int MR, int XS, int WAVES, int TPW>
 void launch_dot_t(const GemmParams &p, hipStream_t s) {
-  auto kern = gemv_dot_kernel<DT, SDT, MR, KMAP>;
+  auto kern = gemv_dot_kernel<DT, SDT, MR, XS, WAVES, TPW>;
   static bool attr_set = false;  // once per instantiation: allow up to 128 KB of dynamic LDS
   if (!attr_set) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               128 * 1024);
     attr_set = true;
   }
-  const size_t lds = std::max(dot_lds_bytes(MR, p.KS), sizeof(float) * 4 * MR * TILE_N);
-  hipLaunchKernelGGL(kern, dim3((p.N + TILE_N - 1) / TILE_N), dim3(256), lds, s, p);
+  const size_t lds = std::max(dot_lds_bytes(MR, p.KS), sizeof(float) * WAVES * MR * TILE_N);
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+  hipLaunchKernelGGL(kern, dim3((tiles + TPW - 1) / TPW), dim3(64 * WAVES), lds, s, p);
+}
+
+template <int DT, int SDT, int MR, int XS>
+void launch_dot_w(const GemmParams &p, int shape, hipStream_t s) {
+  switch (shape) {
+    case DOT_W8_T2: launch_dot_t<DT, SDT, MR, XS, 8, 2>(p, s); break;
+    case DOT_W4_T1: launch_dot_t<DT, SDT, MR, XS, 4, 1>(p, s); break;
+    default: launch_dot_t<DT, SDT, MR, XS, 8, 1>(p, s); break;
+  }
 }
 
 template <int DT, int SDT>
-void launch_dot(const GemmParams &p, hipStream_t s) {
-  const bool km = p.kmap != nullptr;
-  if (p.M == 1) km ? launch_dot_t<DT, SDT, 1, true>(p, s) : launch_dot_t<DT, SDT, 1, false>(p, s);
-  else km ? launch_dot_t<DT, SDT, 2, true>(p, s) : launch_dot_t<DT, SDT, 2, false>(p, s);
+void launch_dot(const GemmParams &p, const Plan &sp, hipStream_t s) {
+  if (p.M == 1) {
+    p.kinv ? launch_dot_w<DT, SDT, 1, XS_SCATTER>(p, sp.waves, s) : launch_dot_w<DT, SDT, 1, XS_CONTIG>(p, sp.waves, s);
+  } else {
+    p.kinv ? launch_dot_w<DT, SDT, 2, XS_SCATTER>(p, sp.waves, s) : launch_dot_w<DT, SDT, 2, XS_CONTIG>(p, sp.waves, s);
+  }
 }
 
 template <int DT, int SDT, int MT>
@@ -787,7 +913,7 @@ void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
 
 template <int DT, int SDT>
 void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
-  if (sp.regime == OC_REGIME_DOT) launch_dot<DT, SDT>(p, s);
+  if (sp.regime == OC_REGIME_DOT) launch_dot<DT, SDT>(p, sp, s);
   else if (sp.regime == OC_REGIME_SPLITK) launch_mfma<DT, SDT>(p, sp.mt, s);
   else launch_tiled<DT, SDT, FMT_GPTQ>(p, sp.tile, s);
 }
@@ -801,13 +927,17 @@ extern "C" {
 size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap,
                                     int32_t regime) {
   if (M <= 0 || N <= 0 || K_phys <= 0 || group_rows <= 0) return 0;
-  return workspace_bytes(plan_gemm(M, N, K_phys, group_rows, has_kmap != 0, regime), M, N, K_phys);
+  // With a kmap the plan depends on whether kinv is given: cover both.
+  const size_t with_kinv = workspace_bytes(plan_gemm(M, N, K_phys, group_rows, has_kmap != 0, regime), M, N, K_phys);
+  if (!has_kmap) return with_kinv;
+  return std::max(with_kinv, workspace_bytes(plan_gemm(M, N, K_phys, group_rows, true, regime, false), M, N, K_phys));
 }
 
 int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
                  const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
-                 int32_t group_rows, const int32_t *kmap, const void *bias, int32_t bias_dtype, void *c,
-                 int64_t ldc, void *workspace, size_t workspace_bytes_given, int32_t regime, void *stream) {
+                 int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
+                 int32_t bias_dtype, void *c, int64_t ldc, void *workspace, size_t workspace_bytes_given,
+                 int32_t regime, void *stream) {
   clear_error();
   if (M < 0 || N <= 0 || K_phys <= 0 || K_logical <= 0)
     return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K_logical=%d K_phys=%d", M, N, K_logical, K_phys);
@@ -827,7 +957,10 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   if (lda < K_logical || ldc < N) return fail(OC_ERR_SHAPE, "lda/ldc smaller than the row length");
   if (lda % 8 != 0 || !aligned(a, 16))
     return fail(OC_ERR_SHAPE, "activations need 16-byte aligned rows (lda %% 8 == 0)");
-  if (!aligned(qt, 16) || !aligned(kmap, 16)) return fail(OC_ERR_SHAPE, "qweight and kmap must be 16-byte aligned");
+  if (!aligned(qt, 16) || !aligned(kmap, 16) || !aligned(kinv, 16))
+    return fail(OC_ERR_SHAPE, "qweight, kmap and kinv must be 16-byte aligned");
+  if (regime == OC_REGIME_DOT && kmap && !kinv)
+    return fail(OC_ERR_INVALID_ARGUMENT, "the decode regime needs kinv with kmap");
   const int64_t tiles = (N + TILE_N - 1) / TILE_N;
   if (tiles * (K_phys / 32) * 64 >= (1LL << 31))
     return fail(OC_ERR_UNSUPPORTED, "layer too large for 32-bit tile offsets");
@@ -839,7 +972,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
                 "(M=%d K_phys=%d group_rows=%d)",
                 M, K_phys, group_rows);
 
-  const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime);
+  const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime, kinv != nullptr);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
   if (need > 0) {
     if (!workspace || workspace_bytes_given < need)
@@ -862,7 +995,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.G = K_phys / group_rows;
   p.group_rows = group_rows;
   p.gshift = ilog2_exact(group_rows / 32);
-  p.kmap = sp.regime == OC_REGIME_DOT ? kmap : nullptr;
+  p.kinv = sp.regime == OC_REGIME_DOT && kmap ? kinv : nullptr;
   p.bias = bias;
   p.bias_dtype = bias_dtype;
   p.c = c;

@@ -82,7 +82,7 @@ SIGNATURES = {
     ),
     "oc_int4_gemm": (
         ctypes.c_int,
-        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _I32,
+        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _I32,
          _P, _I64, _P, _SZ, _I32, _P],
     ),
     "oc_int4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),

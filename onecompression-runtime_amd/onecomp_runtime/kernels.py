@@ -26,6 +26,7 @@ class GroupPlan:
     num_groups: int
     identity: bool
     kmap: np.ndarray  # int32 [k_phys]; -1 marks a zero row
+    kinv: np.ndarray | None  # uint16 [K]: physical row of each input row (k_phys <= 65536)
 
 
 def plan_groups(in_features: int, groupsize: int, g_idx: torch.Tensor | None = None) -> GroupPlan:
@@ -55,7 +56,22 @@ def plan_groups(in_features: int, groupsize: int, g_idx: torch.Tensor | None = N
                                   ctypes.byref(ident)),
         "oc_int4_plan_groups",
     )
-    return GroupPlan(k_phys.value, rows.value, ngroups.value, bool(ident.value), kmap)
+    kinv = None
+    if k_phys.value <= 65536:
+        live = np.nonzero(kmap >= 0)[0]
+        kinv = np.zeros(K, dtype=np.uint16)
+        kinv[kmap[live]] = live.astype(np.uint16)
+    return GroupPlan(k_phys.value, rows.value, ngroups.value, bool(ident.value), kmap, kinv)
+
+
+def row_maps(plan: GroupPlan, device) -> tuple[torch.Tensor | None, torch.Tensor | None]:
+    """Device copies of a plan's kmap (int32) and kinv (uint16 bits in an
+    int16 tensor); both None for the identity layout."""
+    if plan.identity:
+        return None, None
+    kmap = torch.from_numpy(plan.kmap).to(device)
+    kinv = None if plan.kinv is None else torch.from_numpy(plan.kinv.view(np.int16)).to(device)
+    return kmap, kinv
 
 
 @dataclass
@@ -159,7 +175,8 @@ def int4_dequant(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tens
 
 
 def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
-              kmap: torch.Tensor | None = None, bias: torch.Tensor | None = None,
+              kmap: torch.Tensor | None = None, kinv: torch.Tensor | None = None,
+              bias: torch.Tensor | None = None,
               out: torch.Tensor | None = None, regime: int = _hip.OC_REGIME_AUTO) -> torch.Tensor:
     """C[M, N] = A @ dequant(W) + bias on the HIP device (fp32 accumulation).
 
@@ -176,7 +193,10 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
     if adt is not torch.bfloat16 and adt is not torch.float16:
         raise ValueError(f"activations must be fp16 or bf16, got {adt}")
     if a_2d.stride(-1) != 1 or a_2d.stride(0) % 8 or a_2d.data_ptr() % 16:
-        a_2d = a_2d.contiguous()
+        # The kernels read 16-byte row segments: copy into rows padded to 8.
+        K = a_2d.shape[1]
+        buf = torch.empty((a_2d.shape[0], (K + 7) // 8 * 8), dtype=adt, device=a_2d.device)
+        a_2d = buf[:, :K].copy_(a_2d)
     M = a_2d.shape[0]
     N = w.N
     if out is None:
@@ -185,7 +205,7 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
     status = _gemm_fn()(
         a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, in_features, qt.data_ptr(), w.st.data_ptr(),
         _DT[w.st.dtype], w.zt.data_ptr(), N, w.k_phys, w.group_rows,
-        None if kmap is None else kmap.data_ptr(),
+        None if kmap is None else kmap.data_ptr(), None if kinv is None else kinv.data_ptr(),
         None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
         out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes, regime,
         _hip.stream_of(idx),

@@ -56,9 +56,11 @@ class _HipGPTQLinear(torch.nn.Module):
         self.num_phys_groups = plan.num_groups
         if scales.dtype not in (torch.float16, torch.bfloat16):
             scales = scales.to(torch.float16)
-        # The kernels read activations through kmap only when the rows moved.
-        kmap = None if plan.identity else torch.from_numpy(plan.kmap).to(qweight.device)
+        # The kernels read activations through kmap (physical -> input row) and
+        # kinv (input -> physical row) only when the rows moved.
+        kmap, kinv = kernels.row_maps(plan, qweight.device)
         self.register_buffer("kmap", kmap, persistent=False)
+        self.register_buffer("kinv", kinv, persistent=False)
         self.register_buffer("qweight_tiled", None)
         self.register_buffer("scales_tiled", None)
         self.register_buffer("zeros_tiled", None)
@@ -108,7 +110,7 @@ class _HipGPTQLinear(torch.nn.Module):
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
         c = kernels.int4_gemm(a_2d, self.tiled(), in_features=self.in_features, kmap=self.kmap,
-                              bias=self.bias)
+                              kinv=self.kinv, bias=self.bias)
         out = c.reshape(*x.shape[:-1], self.out_features)
         if orig_dtype == torch.float32:
             out = out.to(torch.float32)
@@ -145,11 +147,14 @@ class _HipGPTQLinear(torch.nn.Module):
         # (fused_int4_linear.py:1230-1246).
         before = {n: getattr(self, n) for n in ("qweight_tiled", "zeros_tiled", "kmap", "_src_qweight",
                                                 "_src_qzeros")}
+        kinv_before = self.kinv
         result = super()._apply(fn, recurse=recurse)
         for name, old in before.items():
             new = getattr(self, name)
             if new is not None and new.dtype != torch.int32:
                 setattr(self, name, old.to(new.device))
+        if self.kinv is not None and self.kinv.dtype != torch.int16:
+            self.kinv = kinv_before.to(self.kinv.device)
         for name in ("scales_tiled", "_src_scales"):
             t = getattr(self, name)
             if t is not None and t.dtype not in (torch.float16, torch.bfloat16):

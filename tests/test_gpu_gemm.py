@@ -42,8 +42,8 @@ def _oracle_out(layer, x: torch.Tensor, dtype="bf16", bias=None):
 def _gemm_raw(mod, x, regime):
     from onecomp_runtime import kernels
 
-    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, bias=mod.bias,
-                             regime=regime)
+    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, kinv=mod.kinv,
+                             bias=mod.bias, regime=regime)
 
 
 # -- benchmark workloads ------------------------------------------------------
@@ -330,6 +330,36 @@ def test_decode_kernel_matches_oracle(K, N, M, act):
     say(f"decode kernel K={K} N={N} M={M} act={act}")
     assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"dot {K}x{N} M={M}")
     assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), "auto")
+
+
+@pytest.mark.parametrize("K,N,gs,act", [(52, 16, 26, False), (1004, 200, 32, True), (1004, 72, 32, False),
+                                         (12, 8, 32, False), (4100, 64, 128, True)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_kernel_ragged_k(K, N, gs, act, M):
+    """K % 8 != 0 and padded groups: the decode staging scatters the tail rows
+    one by one and leaves padding rows zero."""
+    from onecomp_runtime import synthetic
+
+    layer = synthetic.gptq_layer(K, N, seed=76 + K, groupsize=gs, act_order=act)
+    x = synthetic.activations(M, K, seed=77)
+    mod = _module_for(layer)
+    assert mod.kmap is not None and mod.kinv is not None
+    say(f"decode ragged K={K} N={N} gs={gs} act={act} M={M}")
+    assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"ragged dot K={K}")
+
+
+def test_decode_regime_needs_kinv():
+    from onecomp_runtime import kernels, synthetic
+
+    layer = synthetic.gptq_layer(1024, 64, seed=78, act_order=True)
+    mod = _module_for(layer)
+    x = synthetic.activations(1, 1024, seed=79).to(DEV)
+    say("decode without kinv")
+    with pytest.raises(ValueError):
+        kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, regime=DOT)
+    # AUTO then takes the small-M MFMA path on gathered activations
+    out = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap)
+    assert_gemm_close(out, _oracle_out(layer, x.cpu()), "auto without kinv")
 
 
 @pytest.mark.parametrize("regime", [DOT, SPLITK, TILED])

@@ -65,6 +65,7 @@ def test_plan_groups_default_grouping(K, gs):
     assert np.array_equal(np.sort(valid), np.arange(K))  # every column exactly once
     rows = np.nonzero(p.kmap >= 0)[0]
     assert np.array_equal(rows // p.group_rows, p.kmap[rows] // gs)  # row's group == column's group
+    assert np.array_equal(p.kmap[p.kinv], np.arange(K))  # kinv: each column's physical row
     assert p.identity == (gs % 32 == 0 and K % gs == 0) or (p.identity and K % 32 == 0)
 
 
@@ -77,6 +78,7 @@ def test_plan_groups_act_order_sorts_by_group_stably():
     p = kernels.plan_groups(K, gs, torch.from_numpy(g_idx))
     assert p.k_phys == K and p.group_rows == 32 and not p.identity
     assert np.array_equal(p.kmap, np.argsort(g_idx, kind="stable"))
+    assert np.array_equal(p.kinv[p.kmap], np.arange(p.k_phys))  # kinv inverts kmap
     # identity g_idx is recognised
     p2 = kernels.plan_groups(K, gs, torch.arange(K) // gs)
     assert p2.identity
