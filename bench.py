@@ -9,10 +9,13 @@ more distinct weight bytes than the 256 MB Infinity Cache holds.
 
 ``sub_results`` time the other workloads (decode M=8, M=16 gs32, M=4096 v2
 DiT shapes, odd groupsize 26, RTN linear, RTN embedding, 64-expert MoE).
-``roofline`` is the dominant kernel (the split-K GEMV at K=5120, N=17408,
-M=1) timed with HIP events on the launch stream. ``cpu_baseline`` times the
-CPU oracle (numpy restatement of the reference's packed path) on one pass of
-the M=1 sweep.
+``roofline`` is the dominant kernel (the decode GEMV at K=5120, N=17408,
+M=1) timed with HIP events on the launch stream; its ``traffic`` (HBM bytes
+per launch) is read from ``profiles/gemv_dot_k5120_n17408_traffic.json``,
+written from two rocprofv3 --pmc runs of this script (FETCH_SIZE, WRITE_SIZE)
+scaled by the same counters on a plain copy of known size, which this script
+also launches. ``cpu_baseline`` times the CPU oracle (numpy restatement of
+the reference's packed path) on one pass of the M=1 sweep.
 
     python bench.py [--steps K] [--warmup W] [--workloads all|decode,...]
 """
@@ -36,6 +39,7 @@ METRIC = "int4 GEMM TFLOP/s & weight GB/s at M=1/16/4096; % of MI355X roofline"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
+CALIB_COPY_BYTES = 512 << 20
 DECODE_SHAPES = [(5120, 5120), (5120, 17408), (17408, 5120), (5120, 1024)]
 DIT_SHAPES = [(3072, 3072), (3072, 12288), (12288, 3072)]
 
@@ -149,12 +153,22 @@ def dominant_kernel(dev, built, xs, copies, iters):
         ms = time_ms(lambda i: g.replay(), max(5, iters // (reps * copies)), 3) / (reps * copies)
     K, N = DECODE_SHAPES[idx]
     M = x.shape[0]
-    algo = gptq_bytes(K, N) + K * 4 + M * K * 2 + M * N * 2  # + kmap, activations, output
+    # packed weights + kinv (uint16) + activations + output
+    algo = gptq_bytes(K, N) + K * 2 + M * K * 2 + M * N * 2
     achieved = algo / (ms * 1e-3) / 1e9
+    # Calibration for the --pmc runs: one plain device copy of known size.
+    src = torch.empty(CALIB_COPY_BYTES, dtype=torch.uint8, device=dev)
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+    traffic = None
+    tfile = ROOT / "profiles" / "gemv_dot_k5120_n17408_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "gemv_dot_kernel<bf16,f16,MR=1,kmap>", "shape": f"M={M} K={K} N={N}",
-            "launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": algo}
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "kernel": "gemv_dot_kernel<bf16,f16,MR=1,scatter,8 waves,1 tile>", "shape": f"M={M} K={K} N={N}",
+            "launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": algo,
+            "calibration_copy_bytes": CALIB_COPY_BYTES}
 
 
 def gptq_m16_workload(dev, steps, warmup):
