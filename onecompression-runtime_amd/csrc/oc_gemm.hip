@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 #include <cstdlib>
 
 #include "oc_device.h"
@@ -701,6 +702,200 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
+// Large-M GPTQ kernel. Workgroup tile 128 x 192, 4 waves splitting the
+// columns (3 tiles of 16 each, 8 x 3 MFMA tiles per wave); two workgroups per
+// CU. Every K step's operands (the 128 x 32 activation block, 8 KB, and the
+// 12 tiles' weight words, scales and zeros) are copied global -> LDS by the
+// DMA path (global_load_lds, no registers) into a ring of BIG_NS buffers,
+// BIG_NS - 1 steps ahead. Each wave dequantizes only its own columns, once
+// per step, from LDS.
+//
+// DMA accounting: every wave issues the same 4 DMA instructions per step,
+// with no branch around them (2 x 16 B activations; 16 B weight words, or
+// scales on wave 3; 4 B zero words on wave 3; lanes without a job copy a
+// valid word into a pad; steps past the end reload the last step), and no
+// other vector memory instruction in the loop. So "this wave's copies of step
+// s have landed" is vmcnt <= 4 * (BIG_NS - 2), and a barrier then makes every
+// wave's copies visible. The ring buffers are distinct LDS arrays, and every
+// access names one of them (slot indices are compile-time constants).
+// grid = (ceil(N / 192), ceil(M / 128), ksplit).
+constexpr int BIG_NS = 4;   // LDS ring depth
+constexpr int BIG_WM = 8;   // 16-row MFMA tiles per workgroup
+constexpr int BIG_WN = 3;   // 16-column tiles per wave
+constexpr int BIG_BM = 16 * BIG_WM;
+constexpr int BIG_TILES = 4 * BIG_WN;                // 16-column tiles per workgroup
+constexpr int BIG_DMA = 4;                           // DMA instructions per wave per step
+// Weight slot (dwords): [wave w: 256 words] x 4, then [wave w: 64 dwords] x 4.
+// Waves 0-2 carry the words of tiles 4w..4w+3 (tile-major, 64 words each);
+// wave 3's first part carries the scales (16 halves per tile) and its second
+// part the zero words (2 per tile).
+constexpr int BIG_W_SC = 3 * 256;                    // scales (halves start here)
+constexpr int BIG_W_Z = 4 * 256 + 3 * 64;            // zero words
+constexpr int BIG_W_DW = 4 * 256 + 4 * 64;
+static_assert(BIG_TILES == 12 && BIG_BM == 128, "DMA assignment assumes 12 tiles and 128 rows");
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(1))) void glb_void_t;
+
+// Lane l's bytes at g land at lds + size * l (lds is wave-uniform).
+__device__ __forceinline__ void dma16(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(lds), 16, 0, 0);
+}
+__device__ __forceinline__ void dma4(const void *g, void *lds) {
+  __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(lds), 4, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier without the release fence of __syncthreads (which would
+// wait for every DMA in flight). This wave's LDS reads are complete first, so
+// no other wave's DMA issued after the barrier can overwrite data they read.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+template <int DT, int SDT>
+__global__ __launch_bounds__(256, 2) void gemm_big_kernel(GemmParams p) {
+  constexpr int NS = BIG_NS;
+  static_assert(NS == 4, "four ring arrays");
+  __shared__ __attribute__((aligned(1024))) uint4 A0[BIG_BM * 4], A1[BIG_BM * 4], A2[BIG_BM * 4], A3[BIG_BM * 4];
+  __shared__ __attribute__((aligned(1024))) uint32_t W0[BIG_W_DW], W1[BIG_W_DW], W2[BIG_W_DW], W3[BIG_W_DW];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int quad = lane >> 4, c16 = lane & 15;
+  const int nb = (p.N + 16 * BIG_TILES - 1) / (16 * BIG_TILES);
+  const int flat = xcd_block(blockIdx.y * nb + blockIdx.x, nb * gridDim.y);
+  const int bx = flat % nb, by = flat / nb;
+  const int t0 = bx * BIG_TILES;  // first tile of the workgroup
+  const int m0 = by * BIG_BM;
+  const int ks_begin = blockIdx.z * p.ksteps_per_split;
+  const int ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+
+  // Activation sources: DMA i of wave w copies rows 16 * (2w + i) + lane / 4,
+  // 16-byte part lane % 4 (rows past M re-read row M - 1; never stored).
+  const uint16_t *a = static_cast<const uint16_t *>(p.a);
+  const uint16_t *asrc0, *asrc1;
+  {
+    const int r0 = min(m0 + 32 * wave + (lane >> 2), p.M - 1);
+    const int r1 = min(m0 + 32 * wave + 16 + (lane >> 2), p.M - 1);
+    asrc0 = a + static_cast<int64_t>(r0) * p.lda + 8 * (lane & 3);
+    asrc1 = a + static_cast<int64_t>(r1) * p.lda + 8 * (lane & 3);
+  }
+  // Weight sources (element offsets for K step 0 / group 0; tiles past N
+  // re-read the last tile, lanes without a job re-read their tile's first word).
+  const uint32_t *qw = static_cast<const uint32_t *>(p.qw);
+  const uint16_t *sc = static_cast<const uint16_t *>(p.scales);
+  const uint32_t *zw = static_cast<const uint32_t *>(p.zeros);
+  const bool w3 = wave == 3;
+  const int wt16 = min(t0 + (w3 ? min(lane >> 1, BIG_TILES - 1) : 4 * wave + (lane >> 4)), tiles - 1);
+  const int wt4 = min(t0 + min(lane >> 1, BIG_TILES - 1), tiles - 1);
+  const bool z_job = w3 && lane < 2 * BIG_TILES;
+
+  auto issue = [&](uint4 *ab, uint32_t *wb, int ks) {
+    const int kk = min(ks, ks_end - 1);  // past the end: reload the last step
+    dma16(asrc0 + 32 * kk, ab + 64 * (2 * wave));
+    dma16(asrc1 + 32 * kk, ab + 64 * (2 * wave + 1));
+    const int g = group_of(p, kk);
+    const uint32_t *src16 =
+        w3 ? reinterpret_cast<const uint32_t *>(sc + (static_cast<int64_t>(wt16) * p.G + g) * TILE_N + 8 * (lane & 1))
+           : qw + (static_cast<int64_t>(wt16) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
+    dma16(src16, wb + 256 * wave);
+    const uint32_t *src4 = zw + (static_cast<int64_t>(wt4) * p.G + g) * 2 + (z_job ? (lane & 1) : 0);
+    dma4(src4, wb + 4 * 256 + 64 * wave);
+  };
+
+  v4f32 acc[BIG_WM][BIG_WN];
+#pragma unroll
+  for (int t = 0; t < BIG_WM; ++t)
+#pragma unroll
+    for (int j = 0; j < BIG_WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+
+  // One K step on ring slot U (a compile-time constant).
+  auto step = [&](auto U, int ks) {
+    constexpr int u = decltype(U)::value;
+    constexpr int un = (u + NS - 1) % NS;
+    uint4 *ab = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
+    uint32_t *wb = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
+    uint4 *abn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
+    uint32_t *wbn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
+    wait_vmcnt<BIG_DMA * (NS - 2)>();  // this wave's copies of step ks landed ...
+    barrier_no_fence();                // ... and everyone's; slot un is free again
+    issue(abn, wbn, ks + NS - 1);
+    const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + BIG_W_SC);
+    uint4 b[BIG_WN];
+#pragma unroll
+    for (int j = 0; j < BIG_WN; ++j) {
+      const int tj = BIG_WN * wave + j;  // tile within the workgroup
+      const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
+      const float sv = scale_f32<SDT>(sb[tj * 16 + c16]);
+      const int zv = tile_zero(wb[BIG_W_Z + tj * 2 + (c16 >> 3)], c16);
+      b[j] = dequant8<DT>(q, make_group_param(sv, zv));
+    }
+#pragma unroll
+    for (int t = 0; t < BIG_WM; ++t) {
+      const uint4 av = ab[(16 * t + c16) * 4 + quad];
+#pragma unroll
+      for (int j = 0; j < BIG_WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
+    }
+  };
+
+  issue(A0, W0, ks_begin);
+  issue(A1, W1, ks_begin + 1);
+  issue(A2, W2, ks_begin + 2);
+  const int nsteps = ks_end - ks_begin;
+  const int nfull = nsteps / NS * NS;
+  for (int s0 = 0; s0 < nfull; s0 += NS) {
+    step(ic<0>{}, ks_begin + s0);
+    step(ic<1>{}, ks_begin + s0 + 1);
+    step(ic<2>{}, ks_begin + s0 + 2);
+    step(ic<3>{}, ks_begin + s0 + 3);
+  }
+  const int rem = nsteps - nfull;
+  if (rem > 0) step(ic<0>{}, ks_begin + nfull);
+  if (rem > 1) step(ic<1>{}, ks_begin + nfull + 1);
+  if (rem > 2) step(ic<2>{}, ks_begin + nfull + 2);
+  wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
+
+  // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + 3 wave + j) + c16.
+  const int tw = t0 + BIG_WN * wave;
+  if (p.ksplit == 1) {
+#pragma unroll
+    for (int j = 0; j < BIG_WN; ++j) {
+      const int n = TILE_N * (tw + j) + c16;
+      if (n >= p.N) continue;
+      const float bv = bias_at(p, n);
+#pragma unroll
+      for (int t = 0; t < BIG_WM; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = m0 + 16 * t + 4 * quad + i;
+          if (r < p.M) store_c<DT>(p.c, static_cast<int64_t>(r) * p.ldc + n, acc[t][j][i] + bv);
+        }
+    }
+  } else {
+    float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < BIG_WN; ++j) {
+      const int n = TILE_N * (tw + j) + c16;
+      if (n >= p.N) continue;
+#pragma unroll
+      for (int t = 0; t < BIG_WM; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = m0 + 16 * t + 4 * quad + i;
+          if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MoE routing: stable counting sort of (token, slot) pairs by expert.
 // One workgroup of 256 threads; thread t owns the contiguous pair range
 // [t*per, (t+1)*per), so ranks computed from per-thread prefix counts keep
@@ -784,6 +979,7 @@ struct Plan {
   int ksteps_per_split;
   bool gather;   // activations gathered into physical order first (kmap, MFMA regimes)
   int waves;     // decode kernel: launch shape (DOT_W*_T*)
+  bool big;      // large M: gemm_big_kernel
 };
 
 // The decode kernel takes M <= 2, power-of-two groups of 32-row steps and its
@@ -815,6 +1011,17 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   }
   if (regime == OC_REGIME_SPLITK) {
     sp.mt = std::max(1, (M + 15) / 16);
+    return sp;
+  }
+  static const bool big_disabled = env_int("ONECOMP_HIP_DISABLE_BIG", 0) != 0;
+  if (M >= 256 && !big_disabled) {
+    // Pipelined 128 x 192 kernel; split K only when the grid cannot fill the chip.
+    sp.big = true;
+    const int blocks = ((M + BIG_BM - 1) / BIG_BM) * ((N + 191) / 192);
+    int ksplit = 1;
+    if (blocks < want) ksplit = std::min((want + blocks - 1) / blocks, std::max(1, ksteps / 16));
+    sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
+    sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
     return sp;
   }
   static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
@@ -912,9 +1119,21 @@ void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
 }
 
 template <int DT, int SDT>
+void launch_big(const GemmParams &p, hipStream_t s) {
+  const dim3 grid((p.N + 191) / 192, (p.M + BIG_BM - 1) / BIG_BM, p.ksplit);
+  hipLaunchKernelGGL((gemm_big_kernel<DT, SDT>), grid, dim3(256), 0, s, p);
+  if (p.ksplit > 1) {
+    const int64_t mn = static_cast<int64_t>(p.M) * p.N;
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
+                       s, p);
+  }
+}
+
+template <int DT, int SDT>
 void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
   if (sp.regime == OC_REGIME_DOT) launch_dot<DT, SDT>(p, sp, s);
   else if (sp.regime == OC_REGIME_SPLITK) launch_mfma<DT, SDT>(p, sp.mt, s);
+  else if (sp.big) launch_big<DT, SDT>(p, s);
   else launch_tiled<DT, SDT, FMT_GPTQ>(p, sp.tile, s);
 }
 

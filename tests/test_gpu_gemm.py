@@ -128,6 +128,35 @@ def test_gemm_dequant_bit_exact_one_hot(regime, kind):
     assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
 
 
+@pytest.mark.parametrize("M,K,N,kind", [(256, 1024, 192, "gs32_v1"), (300, 2048, 400, "actorder"),
+                                         (512, 1040, 96, "gs26"), (257, 4096, 64, "v2"), (600, 512, 1000, "gs128")])
+def test_large_m_kernel_one_hot_bit_exact(M, K, N, kind):
+    """The pipelined large-M kernel (M >= 256; split K when the grid is small)
+    reproduces dequantized columns exactly."""
+    from onecomp_runtime import synthetic
+
+    kw = dict(seed=33)
+    if kind == "v2":
+        kw["v1"] = False
+    if kind == "actorder":
+        kw["act_order"] = True
+    if kind == "gs26":
+        kw["groupsize"] = 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16", layer.v1)
+    rng = np.random.default_rng(5)
+    ks = rng.integers(0, K, M)
+    x = torch.zeros((M, K), dtype=torch.bfloat16)
+    x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+    say(f"large-M one-hot M={M} K={K} N={N} kind={kind}")
+    out = _gemm_raw(mod, x.to(DEV), TILED)
+    assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, torch.bfloat16))
+
+
 # -- regimes and shapes -------------------------------------------------------
 @pytest.mark.parametrize("M", [1, 3, 16, 17, 33, 64])
 def test_splitk_and_tiled_agree_with_oracle(M):
