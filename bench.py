@@ -201,12 +201,17 @@ def dit_workload(dev, steps, warmup):
         x = synthetic.activations(4096, K, seed=20281, outliers=True).to(dev)
         with torch.no_grad():
             ms = time_ms(lambda j: mods[0](x), steps, warmup)
+            # Context only: a dense bf16 GEMM of the same shape on an already
+            # dequantized weight, as the vendor library (hipBLASLt) runs it.
+            wd = torch.randn(N, K, dtype=torch.bfloat16, device=dev)
+            ms_ref = time_ms(lambda j: torch.nn.functional.linear(x, wd), steps, warmup)
         flops = 2 * 4096 * K * N
         tf = flops / (ms * 1e-3) / 1e12
-        out[f"K{K}_N{N}"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+        out[f"K{K}_N{N}"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
+                             "dense_bf16_library_TFLOPs": flops / (ms_ref * 1e-3) / 1e12}
         tot_flops += flops
         tot_ms += ms
-        del mods, x
+        del mods, x, wd
     tf = tot_flops / (tot_ms * 1e-3) / 1e12
     out["aggregate"] = {"TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
     return out

@@ -702,37 +702,41 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// Large-M GPTQ kernel. Workgroup tile 128 x 192, 4 waves splitting the
-// columns (3 tiles of 16 each, 8 x 3 MFMA tiles per wave); two workgroups per
-// CU. Every K step's operands (the 128 x 32 activation block, 8 KB, and the
-// 12 tiles' weight words, scales and zeros) are copied global -> LDS by the
-// DMA path (global_load_lds, no registers) into a ring of BIG_NS buffers,
-// BIG_NS - 1 steps ahead. Each wave dequantizes only its own columns, once
-// per step, from LDS.
+// Large-M GPTQ kernel. Workgroup tile 128 x (64 * WN): 4 waves split the
+// columns (WN tiles of 16 each, 8 x WN MFMA tiles per wave). Every K step's
+// operands (the 128 x 32 activation block, 8 KB, and the workgroup's weight
+// words, scales and zeros) are copied global -> LDS by the DMA path
+// (global_load_lds, no registers) into a ring of BIG_NS buffers, BIG_NS - 1
+// steps ahead. Each wave dequantizes only its own columns, once per step,
+// from LDS. WN = 3: two workgroups per CU; WN = 6: one, with half the LDS
+// traffic per MFMA.
 //
-// DMA accounting: every wave issues the same 4 DMA instructions per step,
-// with no branch around them (2 x 16 B activations; 16 B weight words, or
-// scales on wave 3; 4 B zero words on wave 3; lanes without a job copy a
+// DMA accounting: every wave issues the same DMA instructions each step, with
+// no branch around them (see BigLayout: lanes and waves without a job copy a
 // valid word into a pad; steps past the end reload the last step), and no
-// other vector memory instruction in the loop. So "this wave's copies of step
-// s have landed" is vmcnt <= 4 * (BIG_NS - 2), and a barrier then makes every
-// wave's copies visible. The ring buffers are distinct LDS arrays, and every
+// other vector memory instruction in the loop. So "this wave's copies of
+// step s have landed" is vmcnt <= DMA * (BIG_NS - 2), and a barrier then
+// makes every wave's copies visible. The ring buffers are distinct LDS arrays, and every
 // access names one of them (slot indices are compile-time constants).
-// grid = (ceil(N / 192), ceil(M / 128), ksplit).
+// grid = (ceil(N / (64 WN)), ceil(M / 128), ksplit).
 constexpr int BIG_NS = 4;   // LDS ring depth
-constexpr int BIG_WM = 8;   // 16-row MFMA tiles per workgroup
-constexpr int BIG_WN = 3;   // 16-column tiles per wave
-constexpr int BIG_BM = 16 * BIG_WM;
-constexpr int BIG_TILES = 4 * BIG_WN;                // 16-column tiles per workgroup
-constexpr int BIG_DMA = 4;                           // DMA instructions per wave per step
-// Weight slot (dwords): [wave w: 256 words] x 4, then [wave w: 64 dwords] x 4.
-// Waves 0-2 carry the words of tiles 4w..4w+3 (tile-major, 64 words each);
-// wave 3's first part carries the scales (16 halves per tile) and its second
-// part the zero words (2 per tile).
-constexpr int BIG_W_SC = 3 * 256;                    // scales (halves start here)
-constexpr int BIG_W_Z = 4 * 256 + 3 * 64;            // zero words
-constexpr int BIG_W_DW = 4 * 256 + 4 * 64;
-static_assert(BIG_TILES == 12 && BIG_BM == 128, "DMA assignment assumes 12 tiles and 128 rows");
+
+// One weight ring slot, in dwords. Words are tile-major, 64 per tile, from 0.
+// WN = 3: waves 0-2 copy tiles 4w..4w+3 to 256w, wave 3 the scales to SC;
+//         every wave's 4-byte DMA lands at Z + 64w (wave 3's: the zero words).
+// WN = 6: 16-byte DMA X of wave w copies tiles 4w..4w+3 to 256w; DMA Y of
+//         waves 0-1 copies tiles 16 + 4w.. to 1024 + 256w, of wave 2 the
+//         scales to SC (wave 3: a pad); the 4-byte DMA of wave 0 copies the
+//         zero words to Z (waves 1-3: pads).
+template <int WN>
+struct BigLayout {
+  static constexpr int TILES = 4 * WN;  // 16-column tiles per workgroup
+  static constexpr int WDMA = WN == 3 ? 2 : 3;  // weight DMA instructions per wave per step
+  static constexpr int SC = WN == 3 ? 768 : 1536;
+  static constexpr int Z = WN == 3 ? 1024 : 2048;
+  static constexpr int ZREAD = WN == 3 ? Z + 192 : Z;
+  static constexpr int DW = Z + 256;
+};
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 typedef __attribute__((address_space(1))) void glb_void_t;
@@ -759,119 +763,170 @@ __device__ __forceinline__ void barrier_no_fence() { asm volatile("s_waitcnt lgk
 template <int I>
 using ic = std::integral_constant<int, I>;
 
-template <int DT, int SDT>
-__global__ __launch_bounds__(256, 2) void gemm_big_kernel(GemmParams p) {
-  constexpr int NS = BIG_NS;
-  static_assert(NS == 4, "four ring arrays");
-  __shared__ __attribute__((aligned(1024))) uint4 A0[BIG_BM * 4], A1[BIG_BM * 4], A2[BIG_BM * 4], A3[BIG_BM * 4];
-  __shared__ __attribute__((aligned(1024))) uint32_t W0[BIG_W_DW], W1[BIG_W_DW], W2[BIG_W_DW], W3[BIG_W_DW];
+// 16-byte chunk swizzle of the LDS activation rows (64 bytes each): chunk q
+// of row r sits at position q ^ big_swz(r). An MFMA operand read (rows
+// r0..r0+15, one chunk) then touches distinct banks within every group of 8
+// or 16 lanes the LDS serves together (32 or 64 banks of 4 bytes).
+__device__ __forceinline__ int big_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+template <int DT, int SDT, int WM, int WN, int KPS>
+__global__ __launch_bounds__(256, WM == 8 && WN == 3 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
+  // WM 16-row tiles per workgroup; KPS K steps per ring stage (one barrier
+  // per stage); ring depth NS.
+  using L = BigLayout<WN>;
+  constexpr int BM = 16 * WM;
+  constexpr int NS = KPS == 1 ? 4 : 3;
+  constexpr int TILES = L::TILES;
+  constexpr int AST = BM * 4;       // uint4 per K step of activations
+  constexpr int ADMA = BM / 64;     // activation DMAs per wave per K step
+  constexpr int DMA = ADMA + L::WDMA;
+  static_assert((WM == 8 || WM == 16) && (WN == 3 || WN == 6) && (KPS == 1 || KPS == 2), "DMA assignment");
+  __shared__ __attribute__((aligned(1024))) uint4 A0[KPS * AST], A1[KPS * AST], A2[KPS * AST], A3[NS == 4 ? KPS * AST : 1];
+  __shared__ __attribute__((aligned(1024))) uint32_t W0[KPS * L::DW], W1[KPS * L::DW], W2[KPS * L::DW],
+      W3[NS == 4 ? KPS * L::DW : 1];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
-  const int nb = (p.N + 16 * BIG_TILES - 1) / (16 * BIG_TILES);
+  const int nb = (p.N + 16 * TILES - 1) / (16 * TILES);
   const int flat = xcd_block(blockIdx.y * nb + blockIdx.x, nb * gridDim.y);
   const int bx = flat % nb, by = flat / nb;
-  const int t0 = bx * BIG_TILES;  // first tile of the workgroup
-  const int m0 = by * BIG_BM;
+  const int t0 = bx * TILES;  // first tile of the workgroup
+  const int m0 = by * BM;
   const int ks_begin = blockIdx.z * p.ksteps_per_split;
   const int ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
   const int tiles = (p.N + TILE_N - 1) / TILE_N;
 
-  // Activation sources: DMA i of wave w copies rows 16 * (2w + i) + lane / 4,
-  // 16-byte part lane % 4 (rows past M re-read row M - 1; never stored).
+  // Activation sources: DMA i of wave w fills LDS rows 16 (ADMA w + i) + lane / 4,
+  // 16-byte position lane % 4, which holds chunk (position ^ big_swz(row)) of
+  // that row (rows past M re-read row M - 1; never stored).
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
-  const uint16_t *asrc0, *asrc1;
-  {
-    const int r0 = min(m0 + 32 * wave + (lane >> 2), p.M - 1);
-    const int r1 = min(m0 + 32 * wave + 16 + (lane >> 2), p.M - 1);
-    asrc0 = a + static_cast<int64_t>(r0) * p.lda + 8 * (lane & 3);
-    asrc1 = a + static_cast<int64_t>(r1) * p.lda + 8 * (lane & 3);
+  const uint16_t *asrc[ADMA];
+#pragma unroll
+  for (int i = 0; i < ADMA; ++i) {
+    const int l = 16 * (ADMA * wave + i) + (lane >> 2);
+    const int r = min(m0 + l, p.M - 1);
+    asrc[i] = a + static_cast<int64_t>(r) * p.lda + 8 * ((lane & 3) ^ big_swz(l));
   }
-  // Weight sources (element offsets for K step 0 / group 0; tiles past N
-  // re-read the last tile, lanes without a job re-read their tile's first word).
+  // Weight sources. Words: 16-byte DMAs copy 4 tiles each (lane: tile lane / 16,
+  // 16 bytes lane % 16 of its 256). Scales (lane: tile lane / 2, 16 bytes
+  // lane % 2 of its 32) and zero words (lane: tile lane / 2, word lane % 2).
+  // Tiles past N re-read the last tile; lanes without a job re-read a valid word.
   const uint32_t *qw = static_cast<const uint32_t *>(p.qw);
   const uint16_t *sc = static_cast<const uint16_t *>(p.scales);
   const uint32_t *zw = static_cast<const uint32_t *>(p.zeros);
-  const bool w3 = wave == 3;
-  const int wt16 = min(t0 + (w3 ? min(lane >> 1, BIG_TILES - 1) : 4 * wave + (lane >> 4)), tiles - 1);
-  const int wt4 = min(t0 + min(lane >> 1, BIG_TILES - 1), tiles - 1);
-  const bool z_job = w3 && lane < 2 * BIG_TILES;
+  const int tm = min(t0 + min(lane >> 1, TILES - 1), tiles - 1);  // metadata tile of this lane
+  const bool meta_job = lane < 2 * TILES;
+  const int tqx = min(t0 + 4 * wave + (lane >> 4), tiles - 1);
+  const int tqy = min(t0 + 16 + 4 * wave + (lane >> 4), tiles - 1);
+  // Which wave carries the scales (WN = 3: wave 3; WN = 6: wave 2, wave 3 a pad).
+  const bool sc_wave = WN == 3 ? wave == 3 : wave >= 2;
+  const int sc_dst = WN == 3 ? (wave == 3 ? L::SC : 256 * wave) : 1024 + 256 * wave;
 
-  auto issue = [&](uint4 *ab, uint32_t *wb, int ks) {
+  // The copies of one K step into one ring stage part.
+  auto issue1 = [&](uint4 *ab, uint32_t *wb, int ks) {
     const int kk = min(ks, ks_end - 1);  // past the end: reload the last step
-    dma16(asrc0 + 32 * kk, ab + 64 * (2 * wave));
-    dma16(asrc1 + 32 * kk, ab + 64 * (2 * wave + 1));
+#pragma unroll
+    for (int i = 0; i < ADMA; ++i) dma16(asrc[i] + 32 * kk, ab + 64 * (ADMA * wave + i));
     const int g = group_of(p, kk);
-    const uint32_t *src16 =
-        w3 ? reinterpret_cast<const uint32_t *>(sc + (static_cast<int64_t>(wt16) * p.G + g) * TILE_N + 8 * (lane & 1))
-           : qw + (static_cast<int64_t>(wt16) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
-    dma16(src16, wb + 256 * wave);
-    const uint32_t *src4 = zw + (static_cast<int64_t>(wt4) * p.G + g) * 2 + (z_job ? (lane & 1) : 0);
-    dma4(src4, wb + 4 * 256 + 64 * wave);
+    const int64_t tgm = static_cast<int64_t>(tm) * p.G + g;
+    const uint32_t *scs = reinterpret_cast<const uint32_t *>(sc + tgm * TILE_N + 8 * (lane & 1));
+    const uint32_t *zs = zw + tgm * 2 + (meta_job ? (lane & 1) : 0);
+    const uint32_t *qx = qw + (static_cast<int64_t>(tqx) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
+    if constexpr (WN == 3) {
+      dma16(sc_wave ? scs : qx, wb + sc_dst);
+    } else {
+      const uint32_t *qy = qw + (static_cast<int64_t>(tqy) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
+      dma16(qx, wb + 256 * wave);
+      dma16(sc_wave ? scs : qy, wb + sc_dst);
+    }
+    dma4(zs, wb + L::Z + 64 * wave);
+  };
+  auto issue = [&](uint4 *ab, uint32_t *wb, int stage) {
+#pragma unroll
+    for (int h = 0; h < KPS; ++h) issue1(ab + h * AST, wb + h * L::DW, ks_begin + KPS * stage + h);
   };
 
-  v4f32 acc[BIG_WM][BIG_WN];
+  v4f32 acc[WM][WN];
 #pragma unroll
-  for (int t = 0; t < BIG_WM; ++t)
+  for (int t = 0; t < WM; ++t)
 #pragma unroll
-    for (int j = 0; j < BIG_WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
 
-  // One K step on ring slot U (a compile-time constant).
-  auto step = [&](auto U, int ks) {
+  auto compute1 = [&](const uint4 *ab, const uint32_t *wb) {
+    const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + L::SC);
+    uint4 b[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int tj = WN * wave + j;  // tile within the workgroup
+      const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
+      const float sv = scale_f32<SDT>(sb[tj * 16 + c16]);
+      const int zv = tile_zero(wb[L::ZREAD + tj * 2 + (c16 >> 3)], c16);
+      b[j] = dequant8<DT>(q, make_group_param(sv, zv));
+    }
+#pragma unroll
+    for (int t = 0; t < WM; ++t) {
+      const int row = 16 * t + c16;
+      const uint4 av = ab[row * 4 + (quad ^ big_swz(row))];
+#pragma unroll
+      for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
+    }
+  };
+
+  // One ring stage on slot U (a compile-time constant).
+  auto step = [&](auto U, int stage) {
     constexpr int u = decltype(U)::value;
     constexpr int un = (u + NS - 1) % NS;
     uint4 *ab = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
     uint32_t *wb = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
     uint4 *abn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
     uint32_t *wbn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
-    wait_vmcnt<BIG_DMA * (NS - 2)>();  // this wave's copies of step ks landed ...
-    barrier_no_fence();                // ... and everyone's; slot un is free again
-    issue(abn, wbn, ks + NS - 1);
-    const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + BIG_W_SC);
-    uint4 b[BIG_WN];
+    wait_vmcnt<DMA * KPS * (NS - 2)>();  // this wave's copies of the stage landed ...
+    barrier_no_fence();                      // ... and everyone's; slot un is free again
+    issue(abn, wbn, stage + NS - 1);
 #pragma unroll
-    for (int j = 0; j < BIG_WN; ++j) {
-      const int tj = BIG_WN * wave + j;  // tile within the workgroup
-      const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
-      const float sv = scale_f32<SDT>(sb[tj * 16 + c16]);
-      const int zv = tile_zero(wb[BIG_W_Z + tj * 2 + (c16 >> 3)], c16);
-      b[j] = dequant8<DT>(q, make_group_param(sv, zv));
-    }
-#pragma unroll
-    for (int t = 0; t < BIG_WM; ++t) {
-      const uint4 av = ab[(16 * t + c16) * 4 + quad];
-#pragma unroll
-      for (int j = 0; j < BIG_WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
-    }
+    for (int h = 0; h < KPS; ++h)
+      if (ks_begin + KPS * stage + h < ks_end) compute1(ab + h * AST, wb + h * L::DW);
   };
 
-  issue(A0, W0, ks_begin);
-  issue(A1, W1, ks_begin + 1);
-  issue(A2, W2, ks_begin + 2);
-  const int nsteps = ks_end - ks_begin;
-  const int nfull = nsteps / NS * NS;
-  for (int s0 = 0; s0 < nfull; s0 += NS) {
-    step(ic<0>{}, ks_begin + s0);
-    step(ic<1>{}, ks_begin + s0 + 1);
-    step(ic<2>{}, ks_begin + s0 + 2);
-    step(ic<3>{}, ks_begin + s0 + 3);
+  issue(A0, W0, 0);
+  issue(A1, W1, 1);
+  if constexpr (NS == 4) issue(A2, W2, 2);
+  const int nst = (ks_end - ks_begin + KPS - 1) / KPS;  // stages
+  if constexpr (NS == 4) {
+    const int nfull = nst / 4 * 4;
+    for (int s0 = 0; s0 < nfull; s0 += 4) {
+      step(ic<0>{}, s0);
+      step(ic<1>{}, s0 + 1);
+      step(ic<2>{}, s0 + 2);
+      step(ic<3>{}, s0 + 3);
+    }
+    const int rem = nst - nfull;
+    if (rem > 0) step(ic<0>{}, nfull);
+    if (rem > 1) step(ic<1>{}, nfull + 1);
+    if (rem > 2) step(ic<2>{}, nfull + 2);
+  } else {
+    const int nfull = nst / 3 * 3;
+    for (int s0 = 0; s0 < nfull; s0 += 3) {
+      step(ic<0>{}, s0);
+      step(ic<1>{}, s0 + 1);
+      step(ic<2>{}, s0 + 2);
+    }
+    const int rem = nst - nfull;
+    if (rem > 0) step(ic<0>{}, nfull);
+    if (rem > 1) step(ic<1>{}, nfull + 1);
   }
-  const int rem = nsteps - nfull;
-  if (rem > 0) step(ic<0>{}, ks_begin + nfull);
-  if (rem > 1) step(ic<1>{}, ks_begin + nfull + 1);
-  if (rem > 2) step(ic<2>{}, ks_begin + nfull + 2);
   wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
 
-  // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + 3 wave + j) + c16.
-  const int tw = t0 + BIG_WN * wave;
+  // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
+  const int tw = t0 + WN * wave;
   if (p.ksplit == 1) {
 #pragma unroll
-    for (int j = 0; j < BIG_WN; ++j) {
+    for (int j = 0; j < WN; ++j) {
       const int n = TILE_N * (tw + j) + c16;
       if (n >= p.N) continue;
       const float bv = bias_at(p, n);
 #pragma unroll
-      for (int t = 0; t < BIG_WM; ++t)
+      for (int t = 0; t < WM; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m0 + 16 * t + 4 * quad + i;
@@ -881,11 +936,11 @@ __global__ __launch_bounds__(256, 2) void gemm_big_kernel(GemmParams p) {
   } else {
     float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
 #pragma unroll
-    for (int j = 0; j < BIG_WN; ++j) {
+    for (int j = 0; j < WN; ++j) {
       const int n = TILE_N * (tw + j) + c16;
       if (n >= p.N) continue;
 #pragma unroll
-      for (int t = 0; t < BIG_WM; ++t)
+      for (int t = 0; t < WM; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m0 + 16 * t + 4 * quad + i;
@@ -1017,7 +1072,7 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   if (M >= 256 && !big_disabled) {
     // Pipelined 128 x 192 kernel; split K only when the grid cannot fill the chip.
     sp.big = true;
-    const int blocks = ((M + BIG_BM - 1) / BIG_BM) * ((N + 191) / 192);
+    const int blocks = ((M + 127) / 128) * ((N + 191) / 192);
     int ksplit = 1;
     if (blocks < want) ksplit = std::min((want + blocks - 1) / blocks, std::max(1, ksteps / 16));
     sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
@@ -1118,10 +1173,15 @@ void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
   else launch_tiled_t<DT, SDT, 4, 1, FMT>(p, s);
 }
 
+// Launch shape: 128 x 192 tiles, two K steps per stage. Measured on MI355X
+// against 128 x 384 (one workgroup per CU), 256 x 192 (one per CU) and one K
+// step per stage: this one is fastest on the M = 4096 shapes.
+constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 2;
+
 template <int DT, int SDT>
 void launch_big(const GemmParams &p, hipStream_t s) {
-  const dim3 grid((p.N + 191) / 192, (p.M + BIG_BM - 1) / BIG_BM, p.ksplit);
-  hipLaunchKernelGGL((gemm_big_kernel<DT, SDT>), grid, dim3(256), 0, s, p);
+  const dim3 grid((p.N + 64 * BIG_WN - 1) / (64 * BIG_WN), (p.M + 16 * BIG_WM - 1) / (16 * BIG_WM), p.ksplit);
+  hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, BIG_WM, BIG_WN, BIG_KPS>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
     hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
