@@ -167,9 +167,10 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  *   qt/st/zt tiled weights from oc_int4_prepare (scale_dtype F16 or BF16)
  *   kmap     NULL or int32 [K_phys] (device, 16-byte aligned)
  *   kinv     NULL or uint16 [K_logical] (device, 16-byte aligned), the
- *            inverse of kmap: kinv[kmap[k']] = k'. The decode regime stages
- *            activations through it and needs it whenever kmap is given
- *            (OC_REGIME_AUTO picks another regime without it).
+ *            inverse of kmap: kinv[kmap[k']] = k'. Activations are permuted
+ *            through it (coalesced) when given; the decode regime needs it
+ *            whenever kmap is given (OC_REGIME_AUTO picks another regime
+ *            without it).
  *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
  *   c        [M, N] (row stride ldc elements) of a_dtype
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,

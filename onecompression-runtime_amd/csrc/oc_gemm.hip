@@ -381,9 +381,12 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 // j: MFMA j's K dimension runs over octet j of the 4 K steps, and the A
 // operand of lane (quad, r) is x[r, 32*(4qs + quad) + 8j .. +7] to match. One
 // group parameter per lane covers 32 weights.
-template <int DT, int SDT, int MT>
-__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemmParams p) {
-  constexpr int PF = 4;
+template <int DT, int SDT, int MT, int NW>
+__global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemmParams p) {
+  // NW waves split the tile's K. Quad-steps in flight per wave: weights and
+  // the matching activations travel together (the activations are L2 hits,
+  // but only as early as the weights can they hide their latency).
+  constexpr int PF = MT == 1 ? 3 : 2;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int t = xcd_block(blockIdx.x, gridDim.x);
@@ -399,11 +402,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemmParams p) {
     uint4 q;
     uint32_t s;
     uint32_t z;
+    uint4 x[MT][4];
   };
   Stage st[PF];
   auto load = [&](Stage &S, int qs) {
     const int ks = 4 * qs + quad;
-    if (ks < KS) {
+    const bool kin = ks < KS;
+    if (kin) {
       S.q = qt4[ks * TILE_N];
       const int g = group_of(p, ks);
       S.s = stp[g * TILE_N];
@@ -413,58 +418,47 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemmParams p) {
       S.s = 0;
       S.z = 0;
     }
-  };
-  auto load_a = [&](uint4 (&av)[MT][4], int qs) {
-    const int ks = 4 * qs + quad;
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) {
       const int row = 16 * tt + c16;
-      const bool ok = row < M && ks < KS;
+      const bool ok = row < M && kin;
       const uint16_t *src = a + static_cast<int64_t>(row) * p.lda + 32 * ks;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        av[tt][j] = ok ? *reinterpret_cast<const uint4 *>(src + 8 * j) : make_uint4(0, 0, 0, 0);
+        S.x[tt][j] = ok ? *reinterpret_cast<const uint4 *>(src + 8 * j) : make_uint4(0, 0, 0, 0);
     }
   };
 #pragma unroll
   for (int f = 0; f < PF; ++f) {
-    const int qs = wave + 4 * f;
+    const int qs = wave + NW * f;
     if (qs < QS) load(st[f], qs);
   }
   v4f32 acc[MT];
 #pragma unroll
   for (int tt = 0; tt < MT; ++tt) acc[tt] = v4f32{0.f, 0.f, 0.f, 0.f};
-  uint4 av[MT][4];
-  if (wave < QS) load_a(av, wave);
 
-  for (int base = wave; base < QS; base += 4 * PF) {
+  for (int base = wave; base < QS; base += NW * PF) {
 #pragma unroll
     for (int f = 0; f < PF; ++f) {
-      const int qs = base + 4 * f;
+      const int qs = base + NW * f;
       if (qs >= QS) break;
       const Stage cur = st[f];
-      uint4 a_cur[MT][4];
-#pragma unroll
-      for (int tt = 0; tt < MT; ++tt)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a_cur[tt][j] = av[tt][j];
-      if (qs + 4 < QS) load_a(av, qs + 4);
-      if (qs + 4 * PF < QS) load(st[f], qs + 4 * PF);
+      if (qs + NW * PF < QS) load(st[f], qs + NW * PF);
       const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c16));
       const uint32_t qwords[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint4 b = dequant8<DT>(qwords[j], gp);
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt) acc[tt] = mfma16x16x32<DT>(a_cur[tt][j], b, acc[tt]);
+        for (int tt = 0; tt < MT; ++tt) acc[tt] = mfma16x16x32<DT>(cur.x[tt][j], b, acc[tt]);
       }
     }
   }
 
-  // acc[tt][i] = row 16tt + 4*quad + i, column c16. Fixed LDS tree over the 4 waves.
-  __shared__ float red[2][MT * 16][TILE_N + 1];
+  // acc[tt][i] = row 16tt + 4*quad + i, column c16. Fixed LDS tree over the NW waves.
+  __shared__ float red[NW / 2][MT * 16][TILE_N + 1];
 #pragma unroll
-  for (int half = 2; half >= 1; half >>= 1) {
+  for (int half = NW / 2; half >= 1; half >>= 1) {
     if (wave >= half && wave < 2 * half) {
 #pragma unroll
       for (int tt = 0; tt < MT; ++tt)
@@ -1140,18 +1134,30 @@ void launch_dot(const GemmParams &p, const Plan &sp, hipStream_t s) {
   }
 }
 
-template <int DT, int SDT, int MT>
+template <int DT, int SDT, int MT, int NW>
 void launch_mfma_t(const GemmParams &p, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT>), dim3((p.N + TILE_N - 1) / TILE_N), dim3(256), 0, s, p);
+  hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT, NW>), dim3((p.N + TILE_N - 1) / TILE_N), dim3(64 * NW), 0, s,
+                     p);
 }
 
+template <int DT, int SDT, int MT>
+void launch_mfma_w(const GemmParams &p, int nw, hipStream_t s) {
+  if (MT <= 2 && nw >= 8) launch_mfma_t<DT, SDT, MT, 8>(p, s);
+  else launch_mfma_t<DT, SDT, MT, 4>(p, s);
+}
+
+// Waves per workgroup (measured on MI355X): 8 when there are few tiles and
+// the per-lane state is small (M <= 32), else 4.
 template <int DT, int SDT>
 void launch_mfma(const GemmParams &p, int mt, hipStream_t s) {
+  static const int env_nw = env_int("ONECOMP_HIP_MFMA_WAVES", 0);
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+  const int nw = env_nw > 0 ? env_nw : (tiles <= 256 ? 8 : 4);
   switch (mt) {
-    case 1: launch_mfma_t<DT, SDT, 1>(p, s); break;
-    case 2: launch_mfma_t<DT, SDT, 2>(p, s); break;
-    case 3: launch_mfma_t<DT, SDT, 3>(p, s); break;
-    default: launch_mfma_t<DT, SDT, 4>(p, s); break;
+    case 1: launch_mfma_w<DT, SDT, 1>(p, nw, s); break;
+    case 2: launch_mfma_w<DT, SDT, 2>(p, nw, s); break;
+    case 3: launch_mfma_w<DT, SDT, 3>(p, nw, s); break;
+    default: launch_mfma_w<DT, SDT, 4>(p, nw, s); break;
   }
 }
 
@@ -1282,7 +1288,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.ksplit = sp.ksplit;
   p.ksteps_per_split = sp.ksteps_per_split;
   if (sp.gather) {
-    launch_gather_cols(a, lda, M, K_logical, kmap, K_phys, workspace, stream);
+    launch_gather_cols(a, lda, M, K_logical, kmap, kinv, K_phys, workspace, stream);
     p.a = workspace;
     p.lda = K_phys;
   }

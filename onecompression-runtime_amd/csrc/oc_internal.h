@@ -28,9 +28,10 @@ inline size_t dtype_bytes(int dt) {
     default: return 0;
   }
 }
-// Activation gather into physical row order (oc_layout.hip).
-void launch_gather_cols(const void *a, int64_t lda, int M, int K_logical, const int32_t *kmap, int K_phys,
-                        void *out, void *stream);
+// Activations into physical row order (oc_layout.hip): through kinv when
+// given (coalesced), else through kmap.
+void launch_gather_cols(const void *a, int64_t lda, int M, int K_logical, const int32_t *kmap,
+                        const uint16_t *kinv, int K_phys, void *out, void *stream);
 
 inline bool aligned(const void *p, size_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;

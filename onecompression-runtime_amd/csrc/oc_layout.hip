@@ -120,12 +120,58 @@ __global__ __launch_bounds__(256) void gather_cols_kernel(const uint16_t *__rest
 }
 }  // namespace
 
-void launch_gather_cols(const void *a, int64_t lda, int M, int K_logical, const int32_t *kmap, int K_phys,
-                        void *out, void *stream) {
+namespace {
+// The same permutation by rows through the inverse map: one workgroup per
+// activation row reads the row and kinv contiguously, scatters into LDS
+// (physical order; rows without a source stay zero) and writes the physical
+// row out contiguously. Every global access is coalesced, unlike the gather's
+// one cache line per lane.
+constexpr int SCATTER_ROW_MAX = 32768;  // physical rows per LDS row buffer (64 KB)
+
+__global__ __launch_bounds__(1024) void scatter_rows_kernel(const uint16_t *__restrict__ a, int64_t lda,
+                                                            int K_logical, const uint16_t *__restrict__ kinv,
+                                                            int K_phys, uint16_t *__restrict__ out) {
+  __shared__ __attribute__((aligned(16))) uint16_t row[SCATTER_ROW_MAX];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  uint4 *row4 = reinterpret_cast<uint4 *>(row);
+  if (K_phys != K_logical)
+    for (int i = tid; i < K_phys / 8; i += blockDim.x) row4[i] = make_uint4(0, 0, 0, 0);
+  __syncthreads();
+  const uint16_t *src = a + static_cast<int64_t>(m) * lda;
+  // Octets of 8 logical rows (16-byte loads of the row and of kinv), then the K % 8 tail.
+  const int octets = K_logical >> 3;
+  for (int o = tid; o < octets; o += blockDim.x) {
+    const uint4 xv = reinterpret_cast<const uint4 *>(src)[o];
+    const uint4 rv = reinterpret_cast<const uint4 *>(kinv)[o];
+    const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, rw[4] = {rv.x, rv.y, rv.z, rv.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r0 = static_cast<int>(rw[j] & 0xFFFFu), r1 = static_cast<int>(rw[j] >> 16);
+      if (r0 < K_phys) row[r0] = static_cast<uint16_t>(xw[j]);
+      if (r1 < K_phys) row[r1] = static_cast<uint16_t>(xw[j] >> 16);
+    }
+  }
+  for (int k = 8 * octets + tid; k < K_logical; k += blockDim.x) {
+    const int r = kinv[k];
+    if (r < K_phys) row[r] = src[k];
+  }
+  __syncthreads();
+  uint4 *dst = reinterpret_cast<uint4 *>(out + static_cast<int64_t>(m) * K_phys);
+  for (int i = tid; i < K_phys / 8; i += blockDim.x) dst[i] = row4[i];
+}
+}  // namespace
+
+void launch_gather_cols(const void *a, int64_t lda, int M, int K_logical, const int32_t *kmap,
+                        const uint16_t *kinv, int K_phys, void *out, void *stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (kinv && K_phys <= SCATTER_ROW_MAX) {
+    hipLaunchKernelGGL(scatter_rows_kernel, dim3(M), dim3(1024), 0, s, static_cast<const uint16_t *>(a), lda,
+                       K_logical, kinv, K_phys, static_cast<uint16_t *>(out));
+    return;
+  }
   const int64_t total = static_cast<int64_t>(M) * K_phys;
-  hipLaunchKernelGGL(gather_cols_kernel, dim3(grid_of(total)), dim3(256), 0, static_cast<hipStream_t>(stream),
-                     static_cast<const uint16_t *>(a), lda, M, K_logical, kmap, K_phys,
-                     static_cast<uint16_t *>(out));
+  hipLaunchKernelGGL(gather_cols_kernel, dim3(grid_of(total)), dim3(256), 0, s, static_cast<const uint16_t *>(a),
+                     lda, M, K_logical, kmap, K_phys, static_cast<uint16_t *>(out));
 }
 
 }  // namespace oc
