@@ -208,12 +208,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
     S.s = stp[g * TILE_N];
     S.z = ztp[g * 2];
   };
+  // Prefetches past the end re-read the last step (no branch around loads).
+  const int ks_last = max(ks_end - 1, 0);
   // The head of the weight stream is in flight while activations stage.
 #pragma unroll
-  for (int f = 0; f < DOT_PF; ++f) {
-    const int ks = lp + NPH * f;
-    if (ks < ks_end) load(st[f], ks);
-  }
+  for (int f = 0; f < DOT_PF; ++f) load(st[f], min(lp + NPH * f, ks_last));
 
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
   if constexpr (XS == XS_CONTIG) {
@@ -317,10 +316,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
       const int ks = base + NPH * f;
       if (ks >= ks_end) break;
       const Stage cur = st[f];
-      if (ks + NPH * DOT_PF < ks_end) load(st[f], ks + NPH * DOT_PF);
-      float d[MR];
+      load(st[f], min(ks + NPH * DOT_PF, ks_last));
+      // Two partial sums per row (words 0-1 and 2-3) shorten the dot2 chain.
+      float d[MR][2];
 #pragma unroll
-      for (int m = 0; m < MR; ++m) d[m] = 0.f;
+      for (int m = 0; m < MR; ++m) d[m][0] = d[m][1] = 0.f;
       const uint32_t qs[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
@@ -332,10 +332,11 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
           const uint4 xp = xpairs[(m * KS + ks) * 4 + w];
-          d[m] = dot2acc<DT>(b0, xp.x, d[m]);
-          d[m] = dot2acc<DT>(b1, xp.y, d[m]);
-          d[m] = dot2acc<DT>(b2, xp.z, d[m]);
-          d[m] = dot2acc<DT>(b3, xp.w, d[m]);
+          float &dd = d[m][w >> 1];
+          dd = dot2acc<DT>(b0, xp.x, dd);
+          dd = dot2acc<DT>(b1, xp.y, dd);
+          dd = dot2acc<DT>(b2, xp.z, dd);
+          dd = dot2acc<DT>(b3, xp.w, dd);
         }
       }
       const float zf = static_cast<float>(tile_zero(cur.z, c));
@@ -343,7 +344,7 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         const float2 xs = xsum[m * KSP + ks];
-        acc[m] = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, d[m] - xs.y), acc[m]);
+        acc[m] = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, (d[m][0] + d[m][1]) - xs.y), acc[m]);
       }
     }
   }
@@ -763,10 +764,11 @@ using ic = std::integral_constant<int, I>;
 // or 16 lanes the LDS serves together (32 or 64 banks of 4 bytes).
 __device__ __forceinline__ int big_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
-template <int DT, int SDT, int WM, int WN, int KPS>
-__global__ __launch_bounds__(256, WM == 8 && WN == 3 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
+template <int DT, int SDT, int WM, int WN, int KPS, bool MOE>
+__global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
   // WM 16-row tiles per workgroup; KPS K steps per ring stage (one barrier
-  // per stage); ring depth NS.
+  // per stage); ring depth NS. MOE: grid z = expert; the workgroup walks its
+  // expert's routed rows (expert_offsets / sorted_pairs) in blocks of 16 WM.
   using L = BigLayout<WN>;
   constexpr int BM = 16 * WM;
   constexpr int NS = KPS == 1 ? 4 : 3;
@@ -774,7 +776,8 @@ __global__ __launch_bounds__(256, WM == 8 && WN == 3 ? 2 : 1) void gemm_big_kern
   constexpr int AST = BM * 4;       // uint4 per K step of activations
   constexpr int ADMA = BM / 64;     // activation DMAs per wave per K step
   constexpr int DMA = ADMA + L::WDMA;
-  static_assert((WM == 8 || WM == 16) && (WN == 3 || WN == 6) && (KPS == 1 || KPS == 2), "DMA assignment");
+  static_assert((WM == 4 || WM == 8 || WM == 16) && (WN == 3 || WN == 6) && (KPS == 1 || KPS == 2),
+                "DMA assignment");
   __shared__ __attribute__((aligned(1024))) uint4 A0[KPS * AST], A1[KPS * AST], A2[KPS * AST], A3[NS == 4 ? KPS * AST : 1];
   __shared__ __attribute__((aligned(1024))) uint32_t W0[KPS * L::DW], W1[KPS * L::DW], W2[KPS * L::DW],
       W3[NS == 4 ? KPS * L::DW : 1];
@@ -782,165 +785,187 @@ __global__ __launch_bounds__(256, WM == 8 && WN == 3 ? 2 : 1) void gemm_big_kern
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int nb = (p.N + 16 * TILES - 1) / (16 * TILES);
-  const int flat = xcd_block(blockIdx.y * nb + blockIdx.x, nb * gridDim.y);
+  const int flat = MOE ? static_cast<int>(blockIdx.x) : xcd_block(blockIdx.y * nb + blockIdx.x, nb * gridDim.y);
   const int bx = flat % nb, by = flat / nb;
   const int t0 = bx * TILES;  // first tile of the workgroup
-  const int m0 = by * BM;
-  const int ks_begin = blockIdx.z * p.ksteps_per_split;
-  const int ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
+  const int ks_begin = MOE ? 0 : blockIdx.z * p.ksteps_per_split;
+  const int ks_end = MOE ? p.KS : min(ks_begin + p.ksteps_per_split, p.KS);
   const int tiles = (p.N + TILE_N - 1) / TILE_N;
-
-  // Activation sources: DMA i of wave w fills LDS rows 16 (ADMA w + i) + lane / 4,
-  // 16-byte position lane % 4, which holds chunk (position ^ big_swz(row)) of
-  // that row (rows past M re-read row M - 1; never stored).
-  const uint16_t *a = static_cast<const uint16_t *>(p.a);
-  const uint16_t *asrc[ADMA];
-#pragma unroll
-  for (int i = 0; i < ADMA; ++i) {
-    const int l = 16 * (ADMA * wave + i) + (lane >> 2);
-    const int r = min(m0 + l, p.M - 1);
-    asrc[i] = a + static_cast<int64_t>(r) * p.lda + 8 * ((lane & 3) ^ big_swz(l));
-  }
-  // Weight sources. Words: 16-byte DMAs copy 4 tiles each (lane: tile lane / 16,
-  // 16 bytes lane % 16 of its 256). Scales (lane: tile lane / 2, 16 bytes
-  // lane % 2 of its 32) and zero words (lane: tile lane / 2, word lane % 2).
-  // Tiles past N re-read the last tile; lanes without a job re-read a valid word.
+  int row_begin = by * BM, row_end = p.M;
   const uint32_t *qw = static_cast<const uint32_t *>(p.qw);
   const uint16_t *sc = static_cast<const uint16_t *>(p.scales);
   const uint32_t *zw = static_cast<const uint32_t *>(p.zeros);
-  const int tm = min(t0 + min(lane >> 1, TILES - 1), tiles - 1);  // metadata tile of this lane
-  const bool meta_job = lane < 2 * TILES;
-  const int tqx = min(t0 + 4 * wave + (lane >> 4), tiles - 1);
-  const int tqy = min(t0 + 16 + 4 * wave + (lane >> 4), tiles - 1);
-  // Which wave carries the scales (WN = 3: wave 3; WN = 6: wave 2, wave 3 a pad).
-  const bool sc_wave = WN == 3 ? wave == 3 : wave >= 2;
-  const int sc_dst = WN == 3 ? (wave == 3 ? L::SC : 256 * wave) : 1024 + 256 * wave;
-
-  // The copies of one K step into one ring stage part.
-  auto issue1 = [&](uint4 *ab, uint32_t *wb, int ks) {
-    const int kk = min(ks, ks_end - 1);  // past the end: reload the last step
-#pragma unroll
-    for (int i = 0; i < ADMA; ++i) dma16(asrc[i] + 32 * kk, ab + 64 * (ADMA * wave + i));
-    const int g = group_of(p, kk);
-    const int64_t tgm = static_cast<int64_t>(tm) * p.G + g;
-    const uint32_t *scs = reinterpret_cast<const uint32_t *>(sc + tgm * TILE_N + 8 * (lane & 1));
-    const uint32_t *zs = zw + tgm * 2 + (meta_job ? (lane & 1) : 0);
-    const uint32_t *qx = qw + (static_cast<int64_t>(tqx) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
-    if constexpr (WN == 3) {
-      dma16(sc_wave ? scs : qx, wb + sc_dst);
-    } else {
-      const uint32_t *qy = qw + (static_cast<int64_t>(tqy) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
-      dma16(qx, wb + 256 * wave);
-      dma16(sc_wave ? scs : qy, wb + sc_dst);
-    }
-    dma4(zs, wb + L::Z + 64 * wave);
-  };
-  auto issue = [&](uint4 *ab, uint32_t *wb, int stage) {
-#pragma unroll
-    for (int h = 0; h < KPS; ++h) issue1(ab + h * AST, wb + h * L::DW, ks_begin + KPS * stage + h);
-  };
-
-  v4f32 acc[WM][WN];
-#pragma unroll
-  for (int t = 0; t < WM; ++t)
-#pragma unroll
-    for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
-
-  auto compute1 = [&](const uint4 *ab, const uint32_t *wb) {
-    const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + L::SC);
-    uint4 b[WN];
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int tj = WN * wave + j;  // tile within the workgroup
-      const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
-      const float sv = scale_f32<SDT>(sb[tj * 16 + c16]);
-      const int zv = tile_zero(wb[L::ZREAD + tj * 2 + (c16 >> 3)], c16);
-      b[j] = dequant8<DT>(q, make_group_param(sv, zv));
-    }
-#pragma unroll
-    for (int t = 0; t < WM; ++t) {
-      const int row = 16 * t + c16;
-      const uint4 av = ab[row * 4 + (quad ^ big_swz(row))];
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
-    }
-  };
-
-  // One ring stage on slot U (a compile-time constant).
-  auto step = [&](auto U, int stage) {
-    constexpr int u = decltype(U)::value;
-    constexpr int un = (u + NS - 1) % NS;
-    uint4 *ab = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
-    uint32_t *wb = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
-    uint4 *abn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
-    uint32_t *wbn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
-    wait_vmcnt<DMA * KPS * (NS - 2)>();  // this wave's copies of the stage landed ...
-    barrier_no_fence();                      // ... and everyone's; slot un is free again
-    issue(abn, wbn, stage + NS - 1);
-#pragma unroll
-    for (int h = 0; h < KPS; ++h)
-      if (ks_begin + KPS * stage + h < ks_end) compute1(ab + h * AST, wb + h * L::DW);
-  };
-
-  issue(A0, W0, 0);
-  issue(A1, W1, 1);
-  if constexpr (NS == 4) issue(A2, W2, 2);
-  const int nst = (ks_end - ks_begin + KPS - 1) / KPS;  // stages
-  if constexpr (NS == 4) {
-    const int nfull = nst / 4 * 4;
-    for (int s0 = 0; s0 < nfull; s0 += 4) {
-      step(ic<0>{}, s0);
-      step(ic<1>{}, s0 + 1);
-      step(ic<2>{}, s0 + 2);
-      step(ic<3>{}, s0 + 3);
-    }
-    const int rem = nst - nfull;
-    if (rem > 0) step(ic<0>{}, nfull);
-    if (rem > 1) step(ic<1>{}, nfull + 1);
-    if (rem > 2) step(ic<2>{}, nfull + 2);
-  } else {
-    const int nfull = nst / 3 * 3;
-    for (int s0 = 0; s0 < nfull; s0 += 3) {
-      step(ic<0>{}, s0);
-      step(ic<1>{}, s0 + 1);
-      step(ic<2>{}, s0 + 2);
-    }
-    const int rem = nst - nfull;
-    if (rem > 0) step(ic<0>{}, nfull);
-    if (rem > 1) step(ic<1>{}, nfull + 1);
+  if constexpr (MOE) {
+    const int e = blockIdx.z;
+    row_begin = p.expert_offsets[e];
+    row_end = p.expert_offsets[e + 1];
+    qw += e * p.qw_expert_stride;
+    sc += e * p.s_expert_stride;
+    zw += e * p.z_expert_stride;
   }
-  wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
+  // Logical row -> activation row and output row.
+  auto src_row = [&](int r) -> int64_t { return MOE ? p.sorted_pairs[r] / p.topk : r; };
+  auto dst_row = [&](int r) -> int64_t { return MOE ? p.sorted_pairs[r] : r; };
 
-  // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
-  const int tw = t0 + WN * wave;
-  if (p.ksplit == 1) {
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int n = TILE_N * (tw + j) + c16;
-      if (n >= p.N) continue;
-      const float bv = bias_at(p, n);
-#pragma unroll
-      for (int t = 0; t < WM; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = m0 + 16 * t + 4 * quad + i;
-          if (r < p.M) store_c<DT>(p.c, static_cast<int64_t>(r) * p.ldc + n, acc[t][j][i] + bv);
-        }
+  // One block of up to BM rows starting at m0 (all waves, whole K range).
+  auto run = [&](int m0) {
+    // Activation sources: DMA i of wave w fills LDS rows 16 (ADMA w + i) + lane / 4,
+    // 16-byte position lane % 4, which holds chunk (position ^ big_swz(row)) of
+    // that row (rows past the end re-read the last row; never stored).
+    const uint16_t *a = static_cast<const uint16_t *>(p.a);
+    const uint16_t *asrc[ADMA];
+  #pragma unroll
+    for (int i = 0; i < ADMA; ++i) {
+      const int l = 16 * (ADMA * wave + i) + (lane >> 2);
+      const int r = min(m0 + l, row_end - 1);
+      asrc[i] = a + src_row(r) * p.lda + 8 * ((lane & 3) ^ big_swz(l));
+    }
+    // Weight sources. Words: 16-byte DMAs copy 4 tiles each (lane: tile lane / 16,
+    // 16 bytes lane % 16 of its 256). Scales (lane: tile lane / 2, 16 bytes
+    // lane % 2 of its 32) and zero words (lane: tile lane / 2, word lane % 2).
+    // Tiles past N re-read the last tile; lanes without a job re-read a valid word.
+    const int tm = min(t0 + min(lane >> 1, TILES - 1), tiles - 1);  // metadata tile of this lane
+    const bool meta_job = lane < 2 * TILES;
+    const int tqx = min(t0 + 4 * wave + (lane >> 4), tiles - 1);
+    const int tqy = min(t0 + 16 + 4 * wave + (lane >> 4), tiles - 1);
+    // Which wave carries the scales (WN = 3: wave 3; WN = 6: wave 2, wave 3 a pad).
+    const bool sc_wave = WN == 3 ? wave == 3 : wave >= 2;
+    const int sc_dst = WN == 3 ? (wave == 3 ? L::SC : 256 * wave) : 1024 + 256 * wave;
+
+    // The copies of one K step into one ring stage part.
+    auto issue1 = [&](uint4 *ab, uint32_t *wb, int ks) {
+      const int kk = min(ks, ks_end - 1);  // past the end: reload the last step
+  #pragma unroll
+      for (int i = 0; i < ADMA; ++i) dma16(asrc[i] + 32 * kk, ab + 64 * (ADMA * wave + i));
+      const int g = group_of(p, kk);
+      const int64_t tgm = static_cast<int64_t>(tm) * p.G + g;
+      const uint32_t *scs = reinterpret_cast<const uint32_t *>(sc + tgm * TILE_N + 8 * (lane & 1));
+      const uint32_t *zs = zw + tgm * 2 + (meta_job ? (lane & 1) : 0);
+      const uint32_t *qx = qw + (static_cast<int64_t>(tqx) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
+      if constexpr (WN == 3) {
+        dma16(sc_wave ? scs : qx, wb + sc_dst);
+      } else {
+        const uint32_t *qy = qw + (static_cast<int64_t>(tqy) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
+        dma16(qx, wb + 256 * wave);
+        dma16(sc_wave ? scs : qy, wb + sc_dst);
+      }
+      dma4(zs, wb + L::Z + 64 * wave);
+    };
+    auto issue = [&](uint4 *ab, uint32_t *wb, int stage) {
+  #pragma unroll
+      for (int h = 0; h < KPS; ++h) issue1(ab + h * AST, wb + h * L::DW, ks_begin + KPS * stage + h);
+    };
+
+    v4f32 acc[WM][WN];
+  #pragma unroll
+    for (int t = 0; t < WM; ++t)
+  #pragma unroll
+      for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+
+    auto compute1 = [&](const uint4 *ab, const uint32_t *wb) {
+      const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + L::SC);
+      uint4 b[WN];
+  #pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int tj = WN * wave + j;  // tile within the workgroup
+        const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
+        const float sv = scale_f32<SDT>(sb[tj * 16 + c16]);
+        const int zv = tile_zero(wb[L::ZREAD + tj * 2 + (c16 >> 3)], c16);
+        b[j] = dequant8<DT>(q, make_group_param(sv, zv));
+      }
+  #pragma unroll
+      for (int t = 0; t < WM; ++t) {
+        const int row = 16 * t + c16;
+        const uint4 av = ab[row * 4 + (quad ^ big_swz(row))];
+  #pragma unroll
+        for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
+      }
+    };
+
+    // One ring stage on slot U (a compile-time constant).
+    auto step = [&](auto U, int stage) {
+      constexpr int u = decltype(U)::value;
+      constexpr int un = (u + NS - 1) % NS;
+      uint4 *ab = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
+      uint32_t *wb = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
+      uint4 *abn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
+      uint32_t *wbn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
+      wait_vmcnt<DMA * KPS * (NS - 2)>();  // this wave's copies of the stage landed ...
+      barrier_no_fence();                      // ... and everyone's; slot un is free again
+      issue(abn, wbn, stage + NS - 1);
+  #pragma unroll
+      for (int h = 0; h < KPS; ++h)
+        if (ks_begin + KPS * stage + h < ks_end) compute1(ab + h * AST, wb + h * L::DW);
+    };
+
+    issue(A0, W0, 0);
+    issue(A1, W1, 1);
+    if constexpr (NS == 4) issue(A2, W2, 2);
+    const int nst = (ks_end - ks_begin + KPS - 1) / KPS;  // stages
+    if constexpr (NS == 4) {
+      const int nfull = nst / 4 * 4;
+      for (int s0 = 0; s0 < nfull; s0 += 4) {
+        step(ic<0>{}, s0);
+        step(ic<1>{}, s0 + 1);
+        step(ic<2>{}, s0 + 2);
+        step(ic<3>{}, s0 + 3);
+      }
+      const int rem = nst - nfull;
+      if (rem > 0) step(ic<0>{}, nfull);
+      if (rem > 1) step(ic<1>{}, nfull + 1);
+      if (rem > 2) step(ic<2>{}, nfull + 2);
+    } else {
+      const int nfull = nst / 3 * 3;
+      for (int s0 = 0; s0 < nfull; s0 += 3) {
+        step(ic<0>{}, s0);
+        step(ic<1>{}, s0 + 1);
+        step(ic<2>{}, s0 + 2);
+      }
+      const int rem = nst - nfull;
+      if (rem > 0) step(ic<0>{}, nfull);
+      if (rem > 1) step(ic<1>{}, nfull + 1);
+    }
+    wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
+
+    // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
+    const int tw = t0 + WN * wave;
+    if (MOE || p.ksplit == 1) {
+  #pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int n = TILE_N * (tw + j) + c16;
+        if (n >= p.N) continue;
+        const float bv = bias_at(p, n);
+  #pragma unroll
+        for (int t = 0; t < WM; ++t)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = m0 + 16 * t + 4 * quad + i;
+            if (r < row_end) store_c<DT>(p.c, dst_row(r) * p.ldc + n, acc[t][j][i] + bv);
+          }
+      }
+    } else {
+      float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
+  #pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        const int n = TILE_N * (tw + j) + c16;
+        if (n >= p.N) continue;
+  #pragma unroll
+        for (int t = 0; t < WM; ++t)
+  #pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = m0 + 16 * t + 4 * quad + i;
+            if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
+          }
+      }
+    }
+  };
+  if constexpr (MOE) {
+    for (int m0 = row_begin; m0 < row_end; m0 += BM) {
+      run(m0);
+      __syncthreads();  // the next block's prologue reuses the ring
     }
   } else {
-    float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
-#pragma unroll
-    for (int j = 0; j < WN; ++j) {
-      const int n = TILE_N * (tw + j) + c16;
-      if (n >= p.N) continue;
-#pragma unroll
-      for (int t = 0; t < WM; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = m0 + 16 * t + 4 * quad + i;
-          if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
-        }
-    }
+    if (row_begin < row_end) run(row_begin);
   }
 }
 
@@ -1183,11 +1208,14 @@ void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
 // against 128 x 384 (one workgroup per CU), 256 x 192 (one per CU) and one K
 // step per stage: this one is fastest on the M = 4096 shapes.
 constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 2;
+// Grouped experts use the same 128-row blocks: measured faster than 64-row
+// blocks, whose experts with more than 64 routed rows stream their weights twice.
+constexpr int MOE_WM = BIG_WM;
 
 template <int DT, int SDT>
 void launch_big(const GemmParams &p, hipStream_t s) {
   const dim3 grid((p.N + 64 * BIG_WN - 1) / (64 * BIG_WN), (p.M + 16 * BIG_WM - 1) / (16 * BIG_WM), p.ksplit);
-  hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, BIG_WM, BIG_WN, BIG_KPS>), grid, dim3(256), 0, s, p);
+  hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, BIG_WM, BIG_WN, BIG_KPS, false>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
     hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
@@ -1420,18 +1448,17 @@ int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T, int
   p.qw_expert_stride = tiles * p.KS * 64;
   p.s_expert_stride = tiles * p.G * TILE_N;
   p.z_expert_stride = tiles * p.G * 2;
-  constexpr int WM = 6, WN = 4;
-  const dim3 grid((N + 64 * WN - 1) / (64 * WN), 1, E);
+  const dim3 grid((N + 64 * BIG_WN - 1) / (64 * BIG_WN), 1, E);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = x_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
   if (bf && sbf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_BF16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_BF16, OC_DTYPE_BF16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
   else if (bf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_BF16, OC_DTYPE_F16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_BF16, OC_DTYPE_F16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
   else if (sbf)
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_BF16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_F16, OC_DTYPE_BF16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tiled_kernel<OC_DTYPE_F16, OC_DTYPE_F16, WM, WN, FMT_GPTQ, true>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_F16, OC_DTYPE_F16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
