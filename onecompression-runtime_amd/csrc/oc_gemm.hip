@@ -17,6 +17,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <atomic>
 #include <type_traits>
 #include <cstdlib>
 
@@ -168,27 +169,28 @@ __device__ __forceinline__ int xpair_slot(int m, int K_phys, int r) {
   return m * K_phys + (r & ~7) + ((r & 3) << 1) + ((r >> 2) & 1);
 }
 
-template <int DT, int SDT, int MR, int XS, int WAVES, int TPW>
+template <int DT, int SDT, int MR, int XS, int WAVES, int CPW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
-  // 16-byte activation words staged per thread per round trip (registers
-  // beyond the main loop's would cost occupancy).
+  // CPW columns per workgroup: a whole tile (16) or half of one (8; each K
+  // step's half is one 128-byte line), which doubles the workgroups of
+  // narrow layers. 16-byte activation words are staged SB per thread per
+  // round trip (registers beyond the main loop's would cost occupancy).
   constexpr int SB = XS == XS_CONTIG ? 4 : 2;
   constexpr int NT = 64 * WAVES;
-  constexpr int WPT = WAVES / TPW;  // waves per tile
-  constexpr int NPH = 4 * WPT;      // K-step phases per tile
+  constexpr int PPW = 64 / CPW;     // K-step phases per wave
+  constexpr int NPH = PPW * WAVES;  // K-step phases per workgroup
+  constexpr int SPLIT = TILE_N / CPW;
   constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
   extern __shared__ __attribute__((aligned(16))) uint4 dot_lds[];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int c = lane & 15, h = lane >> 4;
-  const int lp = 4 * (wave % WPT) + h;
-  // TPW tiles per workgroup share one activation staging.
-  const int tiles = (p.N + TILE_N - 1) / TILE_N;
-  const int tw = xcd_block(blockIdx.x, gridDim.x) * TPW + wave / WPT;
-  const bool live = tw < tiles;  // the last workgroup may have fewer tiles
-  const int t = live ? tw : tiles - 1;
+  const int cl = lane % CPW, h = lane / CPW;
+  const int lp = PPW * wave + h;
+  const int blk = xcd_block(blockIdx.x, gridDim.x);
+  const int t = blk / SPLIT;
+  const int c = CPW * (blk % SPLIT) + cl;  // column within the tile
   const int n = TILE_N * t + c;
   const int KS = p.KS, M = p.M;
-  const int ks_end = live ? KS : 0;
+  const int ks_end = KS;
   const int KSP = (KS + 1) & ~1;
   uint4 *xpairs = dot_lds;                                          // [MR][KS * 4]
   float2 *xsum = reinterpret_cast<float2 *>(dot_lds + MR * KS * 4);  // [MR][KSP]: (sum, B * sum)
@@ -349,27 +351,26 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
     }
   }
 
-  // Phases h of one wave (xor 16, 32), then the waves through LDS in order.
+  // Phases h of one wave (xor CPW .. 32), then the waves through LDS in order.
 #pragma unroll
-  for (int m = 0; m < MR; ++m) {
-    acc[m] += __shfl_xor(acc[m], 16);
-    acc[m] += __shfl_xor(acc[m], 32);
-  }
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int off = CPW; off < 64; off <<= 1) acc[m] += __shfl_xor(acc[m], off);
   __syncthreads();
-  float(*red)[MR][TILE_N] = reinterpret_cast<float(*)[MR][TILE_N]>(dot_lds);
+  float(*red)[MR][CPW] = reinterpret_cast<float(*)[MR][CPW]>(dot_lds);
   if (h == 0) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) red[wave][m][c] = acc[m];
+    for (int m = 0; m < MR; ++m) red[wave][m][cl] = acc[m];
   }
   __syncthreads();
-  if (wave % WPT != 0 || h != 0 || !live || n >= p.N) return;
+  if (wave != 0 || h != 0 || n >= p.N) return;
   const float bv = bias_at(p, n);
 #pragma unroll
   for (int m = 0; m < MR; ++m) {
     if (m >= M) break;
-    float v = red[wave][m][c];
+    float v = red[0][m][cl];
 #pragma unroll
-    for (int w = 1; w < WPT; ++w) v += red[wave + w][m][c];
+    for (int w = 1; w < WAVES; ++w) v += red[w][m][cl];
     store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bv);
   }
 }
@@ -1043,7 +1044,7 @@ int ilog2_exact(int v) {
 size_t align256(size_t v) { return (v + 255) / 256 * 256; }
 
 // Decode launch shapes: waves per workgroup x tiles per workgroup.
-enum { DOT_W8_T1 = 0, DOT_W8_T2 = 1, DOT_W4_T1 = 2 };
+enum { DOT_W8 = 0, DOT_W8_HALF = 1, DOT_W4 = 2 };
 
 struct Plan {
   int regime;
@@ -1052,7 +1053,7 @@ struct Plan {
   int ksplit;
   int ksteps_per_split;
   bool gather;   // activations gathered into physical order first (kmap, MFMA regimes)
-  int waves;     // decode kernel: launch shape (DOT_W*_T*)
+  int waves;     // decode kernel: launch shape (DOT_W*)
   bool big;      // large M: gemm_big_kernel
 };
 
@@ -1078,9 +1079,12 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   sp.gather = has_kmap && regime != OC_REGIME_DOT;
   if (regime == OC_REGIME_DOT) {
     static const int dot_shape = env_int("ONECOMP_HIP_DOT_SHAPE", -1);
-    // Measured best on MI355X for 1024 <= N <= 17408: 8 waves, one tile per
-    // workgroup. ONECOMP_HIP_DOT_SHAPE overrides (tuning only).
-    sp.waves = dot_shape >= DOT_W8_T1 && dot_shape <= DOT_W4_T1 ? dot_shape : DOT_W8_T1;
+    // 8 waves; half tiles (twice the workgroups) for narrow layers (N < 2048;
+    // wider ones measured faster with whole tiles, which stage activations once
+    // per 16 columns).
+    // ONECOMP_HIP_DOT_SHAPE overrides (tuning only).
+    const int tiles = (N + TILE_N - 1) / TILE_N;
+    sp.waves = dot_shape >= DOT_W8 && dot_shape <= DOT_W4 ? dot_shape : (tiles < 128 ? DOT_W8_HALF : DOT_W8);
     return sp;
   }
   if (regime == OC_REGIME_SPLITK) {
@@ -1127,26 +1131,30 @@ size_t workspace_bytes(const Plan &sp, int M, int N, int K_phys) {
   return b;
 }
 
-template <int DT, int SDT, int MR, int XS, int WAVES, int TPW>
+template <int DT, int SDT, int MR, int XS, int WAVES, int CPW>
 void launch_dot_t(const GemmParams &p, hipStream_t s) {
-  auto kern = gemv_dot_kernel<DT, SDT, MR, XS, WAVES, TPW>;
-  static bool attr_set = false;  // once per instantiation: allow up to 128 KB of dynamic LDS
-  if (!attr_set) {
+  auto kern = gemv_dot_kernel<DT, SDT, MR, XS, WAVES, CPW>;
+  // Allow up to 128 KB of dynamic LDS, once per instantiation and device.
+  static std::atomic<uint64_t> attr_set{0};
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  const uint64_t bit = dev < 64 ? (uint64_t{1} << dev) : 0;
+  if (!bit || !(attr_set.load(std::memory_order_relaxed) & bit)) {
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
                               128 * 1024);
-    attr_set = true;
+    attr_set.fetch_or(bit, std::memory_order_relaxed);
   }
-  const size_t lds = std::max(dot_lds_bytes(MR, p.KS), sizeof(float) * WAVES * MR * TILE_N);
+  const size_t lds = std::max(dot_lds_bytes(MR, p.KS), sizeof(float) * WAVES * MR * CPW);
   const int tiles = (p.N + TILE_N - 1) / TILE_N;
-  hipLaunchKernelGGL(kern, dim3((tiles + TPW - 1) / TPW), dim3(64 * WAVES), lds, s, p);
+  hipLaunchKernelGGL(kern, dim3(tiles * (TILE_N / CPW)), dim3(64 * WAVES), lds, s, p);
 }
 
 template <int DT, int SDT, int MR, int XS>
 void launch_dot_w(const GemmParams &p, int shape, hipStream_t s) {
   switch (shape) {
-    case DOT_W8_T2: launch_dot_t<DT, SDT, MR, XS, 8, 2>(p, s); break;
-    case DOT_W4_T1: launch_dot_t<DT, SDT, MR, XS, 4, 1>(p, s); break;
-    default: launch_dot_t<DT, SDT, MR, XS, 8, 1>(p, s); break;
+    case DOT_W8_HALF: launch_dot_t<DT, SDT, MR, XS, 8, 8>(p, s); break;
+    case DOT_W4: launch_dot_t<DT, SDT, MR, XS, 4, 16>(p, s); break;
+    default: launch_dot_t<DT, SDT, MR, XS, 8, 16>(p, s); break;
   }
 }
 
