@@ -31,6 +31,7 @@ enum { FMT_GPTQ = 0, FMT_RTN = 1 };
 struct GemmParams {
   const void *a;
   int64_t lda;
+  int64_t a_bytes;  // bytes of the activation block the large-M kernel may read
   int M;
   int K_logical;
   const void *qw;      // GPTQ: tile16 words; RTN: uint8 [N, row_bytes]
@@ -735,14 +736,20 @@ struct BigLayout {
 };
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void glb_void_t;
 
-// Lane l's bytes at g land at lds + size * l (lds is wave-uniform).
-__device__ __forceinline__ void dma16(const void *g, void *lds) {
-  __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(lds), 16, 0, 0);
+// Buffer DMA: lane l's bytes at (resource base + voffset + soffset) land at
+// lds + size * l (lds and soffset wave-uniform). Addresses are 32-bit offsets
+// from a per-tensor resource, so the loop advances them with scalar adds;
+// reads outside the resource's range return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int64_t bytes) {
+  const int n = static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, 0x00020000);
 }
-__device__ __forceinline__ void dma4(const void *g, void *lds) {
-  __builtin_amdgcn_global_load_lds((glb_void_t *)(g), (lds_void_t *)(lds), 4, 0, 0);
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 4, voff, soff, 0, 0);
 }
 
 template <int N>
@@ -783,7 +790,7 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
   __shared__ __attribute__((aligned(1024))) uint32_t W0[KPS * L::DW], W1[KPS * L::DW], W2[KPS * L::DW],
       W3[NS == 4 ? KPS * L::DW : 1];
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int nb = (p.N + 16 * TILES - 1) / (16 * TILES);
   const int flat = MOE ? static_cast<int>(blockIdx.x) : xcd_block(blockIdx.y * nb + blockIdx.x, nb * gridDim.y);
@@ -804,6 +811,10 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
     sc += e * p.s_expert_stride;
     zw += e * p.z_expert_stride;
   }
+  const __amdgpu_buffer_rsrc_t rs_a = buffer_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rs_q = buffer_rsrc(qw, static_cast<int64_t>(tiles) * p.KS * 256);
+  const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(sc, static_cast<int64_t>(tiles) * p.G * 32);
+  const __amdgpu_buffer_rsrc_t rs_z = buffer_rsrc(zw, static_cast<int64_t>(tiles) * p.G * 8);
   // Logical row -> activation row and output row.
   auto src_row = [&](int r) -> int64_t { return MOE ? p.sorted_pairs[r] / p.topk : r; };
   auto dst_row = [&](int r) -> int64_t { return MOE ? p.sorted_pairs[r] : r; };
@@ -813,13 +824,12 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
     // Activation sources: DMA i of wave w fills LDS rows 16 (ADMA w + i) + lane / 4,
     // 16-byte position lane % 4, which holds chunk (position ^ big_swz(row)) of
     // that row (rows past the end re-read the last row; never stored).
-    const uint16_t *a = static_cast<const uint16_t *>(p.a);
-    const uint16_t *asrc[ADMA];
-  #pragma unroll
+    uint32_t avo[ADMA];  // byte offsets into the activations
+#pragma unroll
     for (int i = 0; i < ADMA; ++i) {
       const int l = 16 * (ADMA * wave + i) + (lane >> 2);
       const int r = min(m0 + l, row_end - 1);
-      asrc[i] = a + src_row(r) * p.lda + 8 * ((lane & 3) ^ big_swz(l));
+      avo[i] = static_cast<uint32_t>(src_row(r) * p.lda * 2 + 16 * ((lane & 3) ^ big_swz(l)));
     }
     // Weight sources. Words: 16-byte DMAs copy 4 tiles each (lane: tile lane / 16,
     // 16 bytes lane % 16 of its 256). Scales (lane: tile lane / 2, 16 bytes
@@ -833,40 +843,44 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
     const bool sc_wave = WN == 3 ? wave == 3 : wave >= 2;
     const int sc_dst = WN == 3 ? (wave == 3 ? L::SC : 256 * wave) : 1024 + 256 * wave;
 
+    // Per-lane byte offsets of the weight copies (the K step / group part is
+    // added as a scalar per step).
+    const uint32_t vo_s = static_cast<uint32_t>(tm) * p.G * 32 + 16 * (lane & 1);
+    const uint32_t vo_z = static_cast<uint32_t>(tm) * p.G * 8 + (meta_job ? 4 * (lane & 1) : 0);
+    const uint32_t vo_qx = static_cast<uint32_t>(tqx) * p.KS * 256 + 16 * (lane & 15);
+    const uint32_t vo_qy = static_cast<uint32_t>(tqy) * p.KS * 256 + 16 * (lane & 15);
+
     // The copies of one K step into one ring stage part.
     auto issue1 = [&](uint4 *ab, uint32_t *wb, int ks) {
       const int kk = min(ks, ks_end - 1);  // past the end: reload the last step
-  #pragma unroll
-      for (int i = 0; i < ADMA; ++i) dma16(asrc[i] + 32 * kk, ab + 64 * (ADMA * wave + i));
+#pragma unroll
+      for (int i = 0; i < ADMA; ++i) dma16(rs_a, avo[i], 64 * kk, ab + 64 * (ADMA * wave + i));
       const int g = group_of(p, kk);
-      const int64_t tgm = static_cast<int64_t>(tm) * p.G + g;
-      const uint32_t *scs = reinterpret_cast<const uint32_t *>(sc + tgm * TILE_N + 8 * (lane & 1));
-      const uint32_t *zs = zw + tgm * 2 + (meta_job ? (lane & 1) : 0);
-      const uint32_t *qx = qw + (static_cast<int64_t>(tqx) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
       if constexpr (WN == 3) {
-        dma16(sc_wave ? scs : qx, wb + sc_dst);
+        if (sc_wave) dma16(rs_s, vo_s, 32 * g, wb + sc_dst);
+        else dma16(rs_q, vo_qx, 256 * kk, wb + sc_dst);
       } else {
-        const uint32_t *qy = qw + (static_cast<int64_t>(tqy) * p.KS + kk) * (TILE_N * 4) + 4 * (lane & 15);
-        dma16(qx, wb + 256 * wave);
-        dma16(sc_wave ? scs : qy, wb + sc_dst);
+        dma16(rs_q, vo_qx, 256 * kk, wb + 256 * wave);
+        if (sc_wave) dma16(rs_s, vo_s, 32 * g, wb + sc_dst);
+        else dma16(rs_q, vo_qy, 256 * kk, wb + sc_dst);
       }
-      dma4(zs, wb + L::Z + 64 * wave);
+      dma4(rs_z, vo_z, 8 * g, wb + L::Z + 64 * wave);
     };
     auto issue = [&](uint4 *ab, uint32_t *wb, int stage) {
-  #pragma unroll
+#pragma unroll
       for (int h = 0; h < KPS; ++h) issue1(ab + h * AST, wb + h * L::DW, ks_begin + KPS * stage + h);
     };
 
     v4f32 acc[WM][WN];
-  #pragma unroll
+#pragma unroll
     for (int t = 0; t < WM; ++t)
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
 
     auto compute1 = [&](const uint4 *ab, const uint32_t *wb) {
       const uint16_t *sb = reinterpret_cast<const uint16_t *>(wb + L::SC);
       uint4 b[WN];
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int tj = WN * wave + j;  // tile within the workgroup
         const uint32_t q = wb[tj * 64 + c16 * 4 + quad];
@@ -874,11 +888,11 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
         const int zv = tile_zero(wb[L::ZREAD + tj * 2 + (c16 >> 3)], c16);
         b[j] = dequant8<DT>(q, make_group_param(sv, zv));
       }
-  #pragma unroll
+#pragma unroll
       for (int t = 0; t < WM; ++t) {
         const int row = 16 * t + c16;
         const uint4 av = ab[row * 4 + (quad ^ big_swz(row))];
-  #pragma unroll
+#pragma unroll
         for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
       }
     };
@@ -894,7 +908,7 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
       wait_vmcnt<DMA * KPS * (NS - 2)>();  // this wave's copies of the stage landed ...
       barrier_no_fence();                      // ... and everyone's; slot un is free again
       issue(abn, wbn, stage + NS - 1);
-  #pragma unroll
+#pragma unroll
       for (int h = 0; h < KPS; ++h)
         if (ks_begin + KPS * stage + h < ks_end) compute1(ab + h * AST, wb + h * L::DW);
     };
@@ -931,14 +945,14 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
     // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
     const int tw = t0 + WN * wave;
     if (MOE || p.ksplit == 1) {
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int n = TILE_N * (tw + j) + c16;
         if (n >= p.N) continue;
         const float bv = bias_at(p, n);
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < WM; ++t)
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = m0 + 16 * t + 4 * quad + i;
             if (r < row_end) store_c<DT>(p.c, dst_row(r) * p.ldc + n, acc[t][j][i] + bv);
@@ -946,13 +960,13 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
       }
     } else {
       float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
-  #pragma unroll
+#pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int n = TILE_N * (tw + j) + c16;
         if (n >= p.N) continue;
-  #pragma unroll
+#pragma unroll
         for (int t = 0; t < WM; ++t)
-  #pragma unroll
+#pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = m0 + 16 * t + 4 * quad + i;
             if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
@@ -1063,7 +1077,8 @@ bool dot_eligible(int M, int K_phys, int group_rows) {
   return M >= 1 && M <= 2 && ilog2_exact(group_rows / 32) >= 0 && dot_lds_bytes(M, K_phys / 32) <= 128 * 1024;
 }
 
-Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime, bool has_kinv = true) {
+Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime, bool has_kinv = true,
+               int64_t lda_hint = 0) {
   Plan sp{};
   const int ksteps = K_phys / 32;
   // Tuning knobs, read once per process.
@@ -1092,7 +1107,11 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     return sp;
   }
   static const bool big_disabled = env_int("ONECOMP_HIP_DISABLE_BIG", 0) != 0;
-  if (M >= 256 && !big_disabled) {
+  // The large-M kernel addresses its operands with 32-bit buffer offsets.
+  const int64_t tiles16 = (N + TILE_N - 1) / TILE_N;
+  const bool big_fits = static_cast<int64_t>(M) * std::max<int64_t>(lda_hint, K_phys) * 2 < (int64_t{1} << 31) &&
+                        tiles16 * ksteps * 256 < (int64_t{1} << 31);
+  if (M >= 256 && !big_disabled && big_fits) {
     // Pipelined 128 x 192 kernel; split K only when the grid cannot fill the chip.
     sp.big = true;
     const int blocks = ((M + 127) / 128) * ((N + 191) / 192);
@@ -1212,10 +1231,10 @@ void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
   else launch_tiled_t<DT, SDT, 4, 1, FMT>(p, s);
 }
 
-// Launch shape: 128 x 192 tiles, two K steps per stage. Measured on MI355X
-// against 128 x 384 (one workgroup per CU), 256 x 192 (one per CU) and one K
-// step per stage: this one is fastest on the M = 4096 shapes.
-constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 2;
+// Launch shape: 128 x 192 tiles, one K step per stage (4-deep ring). Measured
+// on MI355X against 128 x 384 (one workgroup per CU), 256 x 192 (one per CU)
+// and two K steps per stage: this one is fastest on the M = 4096 shapes.
+constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 1;
 // Grouped experts use the same 128-row blocks: measured faster than 64-row
 // blocks, whose experts with more than 64 routed rows stream their weights twice.
 constexpr int MOE_WM = BIG_WM;
@@ -1293,7 +1312,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
                 "(M=%d K_phys=%d group_rows=%d)",
                 M, K_phys, group_rows);
 
-  const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime, kinv != nullptr);
+  const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime, kinv != nullptr, lda);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
   if (need > 0) {
     if (!workspace || workspace_bytes_given < need)
@@ -1328,6 +1347,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
     p.a = workspace;
     p.lda = K_phys;
   }
+  p.a_bytes = (static_cast<int64_t>(M) - 1) * p.lda * 2 + static_cast<int64_t>(sp.gather ? K_phys : K_logical) * 2;
   if (sp.ksplit > 1)
     p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + gather_bytes(sp, M, K_phys));
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
@@ -1432,9 +1452,12 @@ int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T, int
     return fail(OC_ERR_SHAPE, "need K %% 32 == 0, group_rows | K (multiple of 32), N %% 64 == 0");
   if (ldx % 8 != 0 || !aligned(x, 16) || ldx < K || ldy < N) return fail(OC_ERR_SHAPE, "x needs 16-byte aligned rows");
   const int64_t tiles = N / TILE_N;
+  if (static_cast<int64_t>(T) * ldx * 2 >= (int64_t{1} << 31) || tiles * (K / 32) * 256 >= (int64_t{1} << 31))
+    return fail(OC_ERR_UNSUPPORTED, "grouped GEMM operands exceed 2 GiB per expert / activation block");
   GemmParams p{};
   p.a = x;
   p.lda = ldx;
+  p.a_bytes = (static_cast<int64_t>(T) - 1) * ldx * 2 + static_cast<int64_t>(K) * 2;
   p.M = T * topk;
   p.K_logical = K;
   p.qw = qt;
