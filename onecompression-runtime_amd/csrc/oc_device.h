@@ -112,31 +112,29 @@ __device__ __forceinline__ GroupParam make_group_param(float s, int zero) {
   return p;
 }
 
+// Codes 0, 1, 4, 5 of a packed word (code i at bits 4i) with one group
+// parameter: returns {codes 0|1, codes 4|5} as packed pairs, each value
+// rounded once (RNE) to DT. Applied to q >> 8 it yields codes 2, 3, 6, 7.
+template <int DT>
+__device__ __forceinline__ uint2 dequant8_half(uint32_t q, GroupParam gp) {
+  const uint32_t magic = 0x64006400u;
+  const v2f16 h0 = bitcast<v2f16>(and_or(q, 0x000F000Fu, magic));  // 1024 + codes 0, 4
+  const v2f16 h1 = bitcast<v2f16>(and_or(q, 0x00F000F0u, magic));  // 1024 + 16 * codes 1, 5
+  const float f0 = __builtin_fmaf(static_cast<float>(h0[0]), gp.s, gp.c);
+  const float f4 = __builtin_fmaf(static_cast<float>(h0[1]), gp.s, gp.c);
+  const float f1 = __builtin_fmaf(static_cast<float>(h1[0]), gp.s16, gp.c16);
+  const float f5 = __builtin_fmaf(static_cast<float>(h1[1]), gp.s16, gp.c16);
+  return uint2{pack2<DT>(f0, f1), pack2<DT>(f4, f5)};
+}
+
 // Dequantize the 8 codes of one packed word (code i at bits 4i) with one
 // group parameter; returns 4 dwords holding the 8 results in natural order
 // (dword d = codes 2d, 2d+1), each rounded once (RNE) to DT.
 template <int DT>
 __device__ __forceinline__ uint4 dequant8(uint32_t q, GroupParam gp) {
-  const uint32_t magic = 0x64006400u;
-  const uint32_t q8 = q >> 8;
-  const v2f16 h0 = bitcast<v2f16>(and_or(q, 0x000F000Fu, magic));   // 1024 + codes 0, 4
-  const v2f16 h1 = bitcast<v2f16>(and_or(q, 0x00F000F0u, magic));   // 1024 + 16 * codes 1, 5
-  const v2f16 h2 = bitcast<v2f16>(and_or(q8, 0x000F000Fu, magic));  // 1024 + codes 2, 6
-  const v2f16 h3 = bitcast<v2f16>(and_or(q8, 0x00F000F0u, magic));  // 1024 + 16 * codes 3, 7
-  const float f0 = __builtin_fmaf(static_cast<float>(h0[0]), gp.s, gp.c);
-  const float f4 = __builtin_fmaf(static_cast<float>(h0[1]), gp.s, gp.c);
-  const float f1 = __builtin_fmaf(static_cast<float>(h1[0]), gp.s16, gp.c16);
-  const float f5 = __builtin_fmaf(static_cast<float>(h1[1]), gp.s16, gp.c16);
-  const float f2 = __builtin_fmaf(static_cast<float>(h2[0]), gp.s, gp.c);
-  const float f6 = __builtin_fmaf(static_cast<float>(h2[1]), gp.s, gp.c);
-  const float f3 = __builtin_fmaf(static_cast<float>(h3[0]), gp.s16, gp.c16);
-  const float f7 = __builtin_fmaf(static_cast<float>(h3[1]), gp.s16, gp.c16);
-  uint4 r;
-  r.x = pack2<DT>(f0, f1);
-  r.y = pack2<DT>(f2, f3);
-  r.z = pack2<DT>(f4, f5);
-  r.w = pack2<DT>(f6, f7);
-  return r;
+  const uint2 lo = dequant8_half<DT>(q, gp);       // codes 0|1, 4|5
+  const uint2 hi = dequant8_half<DT>(q >> 8, gp);  // codes 2|3, 6|7
+  return uint4{lo.x, hi.x, lo.y, hi.y};
 }
 
 // ---- tiled GPTQ layout ("tile16") ---------------------------------------------

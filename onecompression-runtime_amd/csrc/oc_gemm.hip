@@ -21,74 +21,10 @@
 #include <type_traits>
 #include <cstdlib>
 
-#include "oc_device.h"
-#include "oc_internal.h"
+#include "oc_gemm_common.h"
 
 namespace oc {
 
-enum { FMT_GPTQ = 0, FMT_RTN = 1 };
-
-struct GemmParams {
-  const void *a;
-  int64_t lda;
-  int64_t a_bytes;  // bytes of the activation block the large-M kernel may read
-  int M;
-  int K_logical;
-  const void *qw;      // GPTQ: tile16 words; RTN: uint8 [N, row_bytes]
-  const void *scales;  // GPTQ: tile16 16-bit scales; RTN: [N, G] of scale_dtype
-  const void *zeros;   // GPTQ: tile16 zero words; RTN: [N, G] of zero_dtype
-  int scale_dtype;     // RTN (runtime)
-  int zero_dtype;      // RTN (runtime)
-  int rtn_gs;          // RTN: columns per group
-  int rtn_G;           // RTN: groups per row
-  int row_bytes;       // RTN
-  int N;
-  int K_phys;
-  int KS;              // K_phys / 32
-  int G;               // K_phys / group_rows
-  int group_rows;
-  int gshift;          // log2(group_rows / 32), or -1
-  const uint16_t *kinv;  // decode regime: logical -> physical row (NULL: identity)
-  const void *bias;
-  int bias_dtype;
-  void *c;
-  int64_t ldc;
-  float *partials;  // [ksplit, M, N] fp32 (large-M split-K only)
-  int ksplit;
-  int ksteps_per_split;
-  // grouped (MoE) launch
-  const int32_t *expert_offsets;
-  const int32_t *sorted_pairs;
-  int topk;
-  int64_t qw_expert_stride;  // 32-bit words per expert
-  int64_t s_expert_stride;   // 16-bit scales per expert
-  int64_t z_expert_stride;   // zero words per expert
-};
-
-__device__ __forceinline__ int group_of(const GemmParams &p, int ks) {
-  return p.gshift >= 0 ? (ks >> p.gshift) : (32 * ks) / p.group_rows;
-}
-
-template <int SDT>
-__device__ __forceinline__ float scale_f32(uint32_t bits) {
-  return SDT == OC_DTYPE_BF16 ? bf16_to_f32(static_cast<uint16_t>(bits)) : f16_to_f32(static_cast<uint16_t>(bits));
-}
-
-template <int DT>
-__device__ __forceinline__ void store_c(void *c, int64_t i, float v) {
-  static_cast<uint16_t *>(c)[i] = static_cast<uint16_t>(pack2<DT>(v, 0.f));
-}
-
-__device__ __forceinline__ float bias_at(const GemmParams &p, int n) {
-  return p.bias ? load_any_f32(p.bias, n, p.bias_dtype) : 0.f;
-}
-
-// Workgroup order -> tile, keeping neighbouring tiles on one XCD (workgroups
-// are handed to the 8 XCDs round-robin); identity unless 8 divides the count.
-__device__ __forceinline__ int xcd_block(int bid, int nblocks) {
-  if (nblocks % 8 != 0) return bid;
-  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
-}
 
 // ---------------------------------------------------------------------------
 // Decode kernel (M <= 2). grid = tiles, 64*WAVES threads. Lane (c = l%16,
@@ -735,42 +671,6 @@ struct BigLayout {
   static constexpr int DW = Z + 256;
 };
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// Buffer DMA: lane l's bytes at (resource base + voffset + soffset) land at
-// lds + size * l (lds and soffset wave-uniform). Addresses are 32-bit offsets
-// from a per-tensor resource, so the loop advances them with scalar adds;
-// reads outside the resource's range return zero.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int64_t bytes) {
-  const int n = static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, 0x00020000);
-}
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 4, voff, soff, 0, 0);
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
-}
-
-// Workgroup barrier without the release fence of __syncthreads (which would
-// wait for every DMA in flight). This wave's LDS reads are complete first, so
-// no other wave's DMA issued after the barrier can overwrite data they read.
-__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-template <int I>
-using ic = std::integral_constant<int, I>;
-
-// 16-byte chunk swizzle of the LDS activation rows (64 bytes each): chunk q
-// of row r sits at position q ^ big_swz(r). An MFMA operand read (rows
-// r0..r0+15, one chunk) then touches distinct banks within every group of 8
-// or 16 lanes the LDS serves together (32 or 64 banks of 4 bytes).
-__device__ __forceinline__ int big_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
 template <int DT, int SDT, int WM, int WN, int KPS, bool MOE>
 __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
@@ -1069,7 +969,45 @@ struct Plan {
   bool gather;   // activations gathered into physical order first (kmap, MFMA regimes)
   int waves;     // decode kernel: launch shape (DOT_W*)
   bool big;      // large M: gemm_big_kernel
+  int wide_wn;   // large M: gemm_wide_kernel with this many tiles per wave (0: not used)
 };
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  (void)hipGetDevice(&dev);
+  if (dev < 0 || dev >= 64) dev = 0;
+  int v = cached[dev].load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cached[dev].store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+// Tiles per wave of the wide kernel for an M x N problem: the shape whose
+// workgroups fill the compute units best (whole waves of workgroups over the
+// CUs, times the useful fraction of the last column block); ties go to 4.
+int pick_wide_wn(int M, int N) {
+  static const int forced = env_int("ONECOMP_HIP_WIDE_WN", 0);
+  if (forced == 3 || forced == 4) return forced;
+  const int cus = device_cus();
+  double best = -1.0;
+  int pick = 4;
+  for (int wn : {4, 3}) {
+    const int64_t nbn = (N + 64 * wn - 1) / (64 * wn), nbm = (M + 255) / 256;
+    const int64_t blocks = nbn * nbm;
+    const double fill = static_cast<double>(blocks) / (static_cast<double>((blocks + cus - 1) / cus) * cus);
+    const double useful = static_cast<double>(N) / (static_cast<double>(nbn) * 64 * wn);
+    const double score = fill * useful;
+    if (score > best + 1e-9) {
+      best = score;
+      pick = wn;
+    }
+  }
+  return pick;
+}
 
 // The decode kernel takes M <= 2, power-of-two groups of 32-row steps and its
 // activation rows in (at most 128 KB of) LDS.
@@ -1111,6 +1049,12 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   const int64_t tiles16 = (N + TILE_N - 1) / TILE_N;
   const bool big_fits = static_cast<int64_t>(M) * std::max<int64_t>(lda_hint, K_phys) * 2 < (int64_t{1} << 31) &&
                         tiles16 * ksteps * 256 < (int64_t{1} << 31);
+  static const int wide_min_m = env_int("ONECOMP_HIP_WIDE_MIN_M", 1024);
+  if (M >= wide_min_m && wide_min_m > 0 && big_fits && ilog2_exact(group_rows / 32) >= 0) {
+    // 256-row wave tiles, whole K per workgroup.
+    sp.wide_wn = pick_wide_wn(M, N);
+    return sp;
+  }
   if (M >= 256 && !big_disabled && big_fits) {
     // Pipelined 128 x 192 kernel; split K only when the grid cannot fill the chip.
     sp.big = true;
@@ -1351,7 +1295,8 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   if (sp.ksplit > 1)
     p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + gather_bytes(sp, M, K_phys));
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);
+  if (sp.wide_wn) launch_gptq_wide(p, a_dtype, scale_dtype, sp.wide_wn, s);
+  else if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);
   else if (bf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_F16>(p, sp, s);
   else if (sbf) launch_gptq<OC_DTYPE_F16, OC_DTYPE_BF16>(p, sp, s);
   else launch_gptq<OC_DTYPE_F16, OC_DTYPE_F16>(p, sp, s);

@@ -1,0 +1,124 @@
+// Kernel parameters and device helpers shared by the GEMM translation units
+// (oc_gemm.hip, oc_gemm_wide.hip): the launch-parameter block, epilogue
+// helpers, the buffer-resource DMA path into LDS and its wait/barrier
+// primitives.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <type_traits>
+
+#include "oc_device.h"
+#include "oc_internal.h"
+
+namespace oc {
+
+enum { FMT_GPTQ = 0, FMT_RTN = 1 };
+
+struct GemmParams {
+  const void *a;
+  int64_t lda;
+  int64_t a_bytes;  // bytes of the activation block the large-M kernel may read
+  int M;
+  int K_logical;
+  const void *qw;      // GPTQ: tile16 words; RTN: uint8 [N, row_bytes]
+  const void *scales;  // GPTQ: tile16 16-bit scales; RTN: [N, G] of scale_dtype
+  const void *zeros;   // GPTQ: tile16 zero words; RTN: [N, G] of zero_dtype
+  int scale_dtype;     // RTN (runtime)
+  int zero_dtype;      // RTN (runtime)
+  int rtn_gs;          // RTN: columns per group
+  int rtn_G;           // RTN: groups per row
+  int row_bytes;       // RTN
+  int N;
+  int K_phys;
+  int KS;              // K_phys / 32
+  int G;               // K_phys / group_rows
+  int group_rows;
+  int gshift;          // log2(group_rows / 32), or -1
+  const uint16_t *kinv;  // decode regime: logical -> physical row (NULL: identity)
+  const void *bias;
+  int bias_dtype;
+  void *c;
+  int64_t ldc;
+  float *partials;  // [ksplit, M, N] fp32 (large-M split-K only)
+  int ksplit;
+  int ksteps_per_split;
+  // grouped (MoE) launch
+  const int32_t *expert_offsets;
+  const int32_t *sorted_pairs;
+  int topk;
+  int64_t qw_expert_stride;  // 32-bit words per expert
+  int64_t s_expert_stride;   // 16-bit scales per expert
+  int64_t z_expert_stride;   // zero words per expert
+};
+
+__device__ __forceinline__ int group_of(const GemmParams &p, int ks) {
+  return p.gshift >= 0 ? (ks >> p.gshift) : (32 * ks) / p.group_rows;
+}
+
+template <int SDT>
+__device__ __forceinline__ float scale_f32(uint32_t bits) {
+  return SDT == OC_DTYPE_BF16 ? bf16_to_f32(static_cast<uint16_t>(bits)) : f16_to_f32(static_cast<uint16_t>(bits));
+}
+
+template <int DT>
+__device__ __forceinline__ void store_c(void *c, int64_t i, float v) {
+  static_cast<uint16_t *>(c)[i] = static_cast<uint16_t>(pack2<DT>(v, 0.f));
+}
+
+__device__ __forceinline__ float bias_at(const GemmParams &p, int n) {
+  return p.bias ? load_any_f32(p.bias, n, p.bias_dtype) : 0.f;
+}
+
+// Workgroup order -> tile, keeping neighbouring tiles on one XCD (workgroups
+// are handed to the 8 XCDs round-robin); identity unless 8 divides the count.
+__device__ __forceinline__ int xcd_block(int bid, int nblocks) {
+  if (nblocks % 8 != 0) return bid;
+  return (bid & 7) * (nblocks >> 3) + (bid >> 3);
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// Buffer DMA: lane l's bytes at (resource base + voffset + soffset) land at
+// lds + size * l (lds and soffset wave-uniform). Addresses are 32-bit offsets
+// from a per-tensor resource, so the loop advances them with scalar adds;
+// reads outside the resource's range return zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, int64_t bytes) {
+  const int n = static_cast<int>(bytes < 0x7fffffff ? bytes : 0x7fffffff);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), 0, n, 0x00020000);
+}
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma4(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, void *lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t *)(lds), 4, voff, soff, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+
+// Workgroup barrier without the release fence of __syncthreads (which would
+// wait for every DMA in flight). This wave's LDS reads are complete first, so
+// no other wave's DMA issued after the barrier can overwrite data they read.
+__device__ __forceinline__ void barrier_no_fence() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int I>
+using ic = std::integral_constant<int, I>;
+
+// 16-byte chunk swizzle of the LDS activation rows (64 bytes each): chunk q
+// of row r sits at position q ^ big_swz(r). An MFMA operand read (rows
+// r0..r0+15, one chunk) then touches distinct banks within every group of 8
+// or 16 lanes the LDS serves together (32 or 64 banks of 4 bytes).
+__device__ __forceinline__ int big_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
+
+// Host helpers.
+int env_int(const char *name, int dflt);
+
+// Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
+// ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.
+void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);
+
+}  // namespace oc

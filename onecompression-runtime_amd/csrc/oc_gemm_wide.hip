@@ -1,0 +1,318 @@
+// Large-M fused int4 GEMM with 256-row wave tiles for gfx950.
+//
+// Workgroup tile: 256 rows x 64*WN columns, 4 waves (one per SIMD). Each wave
+// owns WN 16-column tiles and all 256 rows, so every weight is dequantized
+// once per workgroup and feeds 256 rows of MFMA work: per 32-row K step a wave
+// issues 16 x WN v_mfma_f32_16x16x32 against WN dequantized B operands and
+// holds 64*WN fp32 accumulators per lane. Dequantization (dequant8: exact fp32
+// product, one RNE) costs ~20 VALU per weight word against 16 MFMAs per word,
+// about a third of the MFMA time, and overlaps it.
+//
+// Operand flow, one 32-row K step per stage:
+//   global -> LDS   buffer DMA (buffer_load ... lds, no registers) into a ring
+//                   of NS slots, NS-1 stages ahead: the 256 x 32 activation
+//                   block (16 KB, 16-byte chunks swizzled per row), the
+//                   workgroup's weight words, scales and zero words;
+//   LDS -> VGPRs    one stage ahead of the MFMAs: while the MFMAs of stage s
+//                   run from one register set, the wave reads stage s+1's A
+//                   fragments and weight words into the other and dequantizes
+//                   them.
+// One barrier per stage. Every wave issues the same number of DMA instructions
+// per stage (lanes and waves without a job read out of the buffer range, which
+// returns zero, into a pad), and no other vector memory instruction runs in the
+// loop, so "this wave's copies of stage s+1 landed" is a fixed vmcnt.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "oc_gemm_common.h"
+
+namespace oc {
+
+constexpr int WIDE_NS = 4;  // LDS ring depth (stages)
+
+// One weight/metadata ring slot, in dwords.
+//   W: 4*WN tiles x 64 words (tile-major, as in global memory)
+//   S: 16-bit scales [tile][16 columns]
+//   Z: zero words [tile][2]
+//   P: pad destination of jobless DMAs
+// DMA jobs per wave and stage (besides the 4 activation DMAs):
+//   WN = 4: 16-byte DMA: wave w copies tiles 4w..4w+3 to W + 256w;
+//           4-byte DMA: waves 0-1 copy the scales of tiles 8w..8w+7 to S + 64w,
+//           wave 2 the zero words to Z (lanes 0-31), wave 3 a pad.
+//   WN = 3: 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 the scales
+//           (lanes 0-23) to S; 4-byte DMA: wave 0 the zero words (lanes 0-23),
+//           waves 1-3 a pad.
+template <int WN>
+struct WideLayout {
+  static constexpr int TILES = 4 * WN;
+  static constexpr int W = 0;
+  static constexpr int S = 256 * WN;
+  static constexpr int Z = S + (WN == 4 ? 128 : 256);
+  static constexpr int P = Z + 64;
+  static constexpr int DW = P + 64;
+};
+
+// A buffer offset no resource reaches (reads return zero, no memory access);
+// voffset + OOB_OFFSET stays below 2^32 because every voffset is below 2^31.
+constexpr uint32_t OOB_OFFSET = 0x80000000u;
+
+template <int DT, int SDT, int WN>
+__global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
+  using L = WideLayout<WN>;
+  constexpr int NS = WIDE_NS;
+  constexpr int BM = 256;
+  constexpr int AST = BM * 4;  // uint4 per activation slot
+  constexpr int DMA = 6;       // DMA instructions per wave and stage
+  static_assert(NS % 2 == 0, "register sets alternate with the ring slots");
+  __shared__ __attribute__((aligned(1024))) uint4 A0[AST], A1[AST], A2[AST], A3[AST];
+  __shared__ __attribute__((aligned(1024))) uint32_t W0[L::DW], W1[L::DW], W2[L::DW], W3[L::DW];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int quad = lane >> 4, c16 = lane & 15;
+  const int nbn = (p.N + 16 * L::TILES - 1) / (16 * L::TILES);
+  const int nbm = (p.M + BM - 1) / BM;
+  const int flat = xcd_block(blockIdx.x, nbn * nbm);
+  const int bx = flat % nbn, by = flat / nbn;
+  const int t0 = bx * L::TILES;
+  const int m0 = by * BM;
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+  const int KS = p.KS;
+
+  const __amdgpu_buffer_rsrc_t rs_a = buffer_rsrc(p.a, p.a_bytes);
+  const __amdgpu_buffer_rsrc_t rs_q = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
+  const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * p.G * 32);
+  const __amdgpu_buffer_rsrc_t rs_z = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * p.G * 8);
+
+  // Activation DMA i of wave w fills rows 16 (4w + i) + lane / 4 of the slot,
+  // 16-byte position lane % 4, with chunk (position ^ big_swz(row)) of the row.
+  // Rows past M re-read row M - 1 (never stored).
+  uint32_t avo[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int l = 16 * (4 * wave + i) + (lane >> 2);
+    const int r = min(m0 + l, p.M - 1);
+    avo[i] = static_cast<uint32_t>(static_cast<int64_t>(r) * p.lda * 2 + 16 * ((lane & 3) ^ big_swz(l)));
+  }
+  // Weight jobs (tiles past N re-read the last tile; never stored).
+  auto tile_at = [&](int t) { return min(t0 + t, tiles - 1); };
+  __amdgpu_buffer_rsrc_t rs_x, rs_y;
+  uint32_t vo_x, vo_y;
+  int x_kind, y_kind;  // 0: words, 1: scales, 2: zeros, 3: pad (soffset selector)
+  int x_dst, y_dst;    // dword offsets in the slot
+  if (WN == 3 && wave == 3) {
+    rs_x = rs_s;
+    vo_x = lane < 24 ? static_cast<uint32_t>(tile_at(lane >> 1)) * p.G * 32 + 16 * (lane & 1) : OOB_OFFSET;
+    x_kind = 1;
+    x_dst = L::S;
+  } else {
+    rs_x = rs_q;
+    vo_x = static_cast<uint32_t>(tile_at(4 * wave + (lane >> 4))) * KS * 256 + 16 * (lane & 15);
+    x_kind = 0;
+    x_dst = L::W + 256 * wave;
+  }
+  if (WN == 4 && wave < 2) {
+    rs_y = rs_s;
+    vo_y = static_cast<uint32_t>(tile_at(8 * wave + (lane >> 3))) * p.G * 32 + 4 * (lane & 7);
+    y_kind = 1;
+    y_dst = L::S + 64 * wave;
+  } else if ((WN == 4 && wave == 2) || (WN == 3 && wave == 0)) {
+    rs_y = rs_z;
+    vo_y = lane < 2 * L::TILES ? static_cast<uint32_t>(tile_at(lane >> 1)) * p.G * 8 + 4 * (lane & 1) : OOB_OFFSET;
+    y_kind = 2;
+    y_dst = L::Z;
+  } else {
+    rs_y = rs_z;
+    vo_y = OOB_OFFSET;
+    y_kind = 3;
+    y_dst = L::P;
+  }
+  auto soff = [&](int kind, int ks, int g) -> uint32_t {
+    return kind == 0 ? 256u * ks : kind == 1 ? 32u * g : kind == 2 ? 8u * g : 0u;
+  };
+
+  // The copies of K step ks into one slot, one DMA instruction at a time
+  // (d = 0-3: activation rows, 4: 16-byte weight job, 5: 4-byte job), so a
+  // stage can spread them out. Past the end the activations read as zero
+  // (out-of-range offset) and the weights repeat the last step, so the
+  // padding steps of the last ring cycle add nothing.
+  auto issue_one = [&](uint4 *as, uint32_t *ws, int ks, int d) {
+    const int kk = min(ks, KS - 1);
+    const int g = kk >> p.gshift;  // the host routes only power-of-two group steps here
+    if (d < 4) dma16(rs_a, avo[d], ks < KS ? 64u * ks : OOB_OFFSET, as + 64 * (4 * wave + d));
+    else if (d == 4) dma16(rs_x, vo_x, soff(x_kind, kk, g), ws + x_dst);
+    else dma4(rs_y, vo_y, soff(y_kind, kk, g), ws + y_dst);
+  };
+  auto issue = [&](uint4 *as, uint32_t *ws, int ks) {
+#pragma unroll
+    for (int d = 0; d < DMA; ++d) issue_one(as, ws, ks, d);
+  };
+
+  // Register state: the A fragments of the 16 row tiles (refilled from the
+  // next stage right after their MFMAs issue, so each read has a whole stage
+  // to land) and two sets of dequantized B operands.
+  uint4 a[16], b0[WN], b1[WN];
+
+  // Weight words, scales and zero words of this wave's tiles for one stage.
+  struct Meta {
+    uint32_t q[WN], zw[WN];
+    uint16_t sv[WN];
+  };
+  auto read_meta = [&](const uint32_t *ws) {
+    const uint16_t *sb = reinterpret_cast<const uint16_t *>(ws + L::S);
+    Meta m;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int tj = WN * wave + j;
+      m.q[j] = ws[L::W + tj * 64 + c16 * 4 + quad];
+      m.sv[j] = sb[tj * 16 + c16];
+      m.zw[j] = ws[L::Z + tj * 2 + (c16 >> 3)];
+    }
+    return m;
+  };
+  auto dequant1 = [&](const Meta &m, int j) {
+    return dequant8<DT>(m.q[j], make_group_param(scale_f32<SDT>(m.sv[j]), tile_zero(m.zw[j], c16)));
+  };  // (prologue)
+  auto read_a = [&](const uint4 *as, int t) {
+    const int row = 16 * t + c16;
+    return as[row * 4 + (quad ^ big_swz(row))];
+  };
+
+  v4f32 acc[16][WN];
+#pragma unroll
+  for (int t = 0; t < 16; ++t)
+#pragma unroll
+    for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+
+  // Stage s computes with the A fragments and B set s % 2 read in the
+  // previous stage, reads stage s + 1 (slot u + 1) behind its MFMAs and
+  // refills slot u (read by every wave before the barrier) with stage s + NS.
+  auto step = [&](auto U, int s) {
+    constexpr int u = decltype(U)::value;
+    constexpr int un = (u + 1) % NS;
+    uint4 *as = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
+    uint32_t *ws = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
+    const uint4 *asn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
+    const uint32_t *wsn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
+    uint4 *bc = u % 2 == 0 ? b0 : b1;
+    uint4 *bn = u % 2 == 0 ? b1 : b0;
+    wait_vmcnt<DMA * (NS - 2)>();  // this wave's copies of stage s + 1 landed ...
+    barrier_no_fence();            // ... and everyone's; slot u is free
+    const Meta m = read_meta(wsn);
+    // Row tile t: its WN MFMAs, each followed by a share of the next stage's
+    // dequantization, then the refill of a[t]; DMA d of stage s + NS issues in
+    // row tile 2d (issued together they queue up behind each other and stall
+    // the wave at the top of the stage). The dequantization of tile j
+    // runs in three parts (group parameter; codes 0, 1, 4, 5; codes 2, 3, 6,
+    // 7) in row tiles 2 + 3j .. 4 + 3j, so VALU work issues while the matrix
+    // pipe is busy. Scheduling barriers keep this order (otherwise the reads
+    // are hoisted, both stages' fragments are live at once, and the VALU work
+    // bunches up between MFMAs).
+    GroupParam gp[WN];
+    uint2 lo[WN];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+#pragma unroll
+      // Weights as the A operand and activations as B: the result tile is
+      // C^T, so a lane holds 4 consecutive output columns of one row.
+      for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(bc[j], a[t], acc[t][j]);
+      a[t] = read_a(asn, t);
+      if (t % 2 == 0 && t / 2 < DMA) issue_one(as, ws, s + NS, t / 2);
+      constexpr int PARTS = 3 * WN;
+      const int part = t - 2;
+      if (part >= 0 && part < PARTS) {
+        const int j = part / 3;
+        if (part % 3 == 0) {
+          gp[j] = make_group_param(scale_f32<SDT>(m.sv[j]), tile_zero(m.zw[j], c16));
+        } else if (part % 3 == 1) {
+          lo[j] = dequant8_half<DT>(m.q[j], gp[j]);
+        } else {
+          const uint2 hi = dequant8_half<DT>(m.q[j] >> 8, gp[j]);
+          bn[j] = uint4{lo[j].x, hi.x, lo[j].y, hi.y};
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < WN; ++j) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+        __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // up to three VALU
+      }
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // the A refill
+      if (t % 2 == 0 && t / 2 < DMA) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // the DMA
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  issue(A0, W0, 0);
+  issue(A1, W1, 1);
+  issue(A2, W2, 2);
+  issue(A3, W3, 3);
+  wait_vmcnt<DMA * (NS - 1)>();
+  barrier_no_fence();
+  {
+    const Meta m = read_meta(W0);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) a[t] = read_a(A0, t);
+#pragma unroll
+    for (int j = 0; j < WN; ++j) b0[j] = dequant1(m, j);
+  }
+  // Whole ring cycles only (no remainder code: it would give the loop's
+  // accumulators other registers and cost copies every iteration).
+  for (int s0 = 0; s0 < KS; s0 += NS) {
+    step(ic<0>{}, s0);
+    step(ic<1>{}, s0 + 1);
+    step(ic<2>{}, s0 + 2);
+    step(ic<3>{}, s0 + 3);
+  }
+  wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
+
+  // Epilogue: acc[t][j][i] = C[m0 + 16t + c16][16 (t0 + WN wave + j) + 4 quad + i]:
+  // four consecutive columns per lane, stored as one 8-byte write when the
+  // output rows allow it (N is a multiple of 8, so a group of four is either
+  // wholly inside N or wholly outside).
+  const bool vec8 = ((reinterpret_cast<uintptr_t>(p.c) | static_cast<uintptr_t>(p.ldc * 2)) & 7) == 0;
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int n0 = TILE_N * (t0 + WN * wave + j) + 4 * quad;
+    if (n0 >= p.N) continue;
+    float bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) bv[i] = bias_at(p, n0 + i);
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int r = m0 + 16 * t + c16;
+      if (r >= p.M) continue;
+      const int64_t off = static_cast<int64_t>(r) * p.ldc + n0;
+      const v4f32 v = acc[t][j];
+      if (vec8) {
+        const uint2 pk{pack2<DT>(v[0] + bv[0], v[1] + bv[1]), pack2<DT>(v[2] + bv[2], v[3] + bv[3])};
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(p.c) + off) = pk;
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) store_c<DT>(p.c, off + i, v[i] + bv[i]);
+      }
+    }
+  }
+}
+
+template <int DT, int SDT, int WN>
+static void launch_wide_t(const GemmParams &p, hipStream_t s) {
+  const int nbn = (p.N + 64 * WN - 1) / (64 * WN), nbm = (p.M + 255) / 256;
+  hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN>), dim3(nbn * nbm), dim3(256), 0, s, p);
+}
+
+template <int DT, int SDT>
+static void launch_wide_d(const GemmParams &p, int wn, hipStream_t s) {
+  if (wn == 3) launch_wide_t<DT, SDT, 3>(p, s);
+  else launch_wide_t<DT, SDT, 4>(p, s);
+}
+
+void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s) {
+  const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
+  if (bf && sbf) launch_wide_d<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, wn, s);
+  else if (bf) launch_wide_d<OC_DTYPE_BF16, OC_DTYPE_F16>(p, wn, s);
+  else if (sbf) launch_wide_d<OC_DTYPE_F16, OC_DTYPE_BF16>(p, wn, s);
+  else launch_wide_d<OC_DTYPE_F16, OC_DTYPE_F16>(p, wn, s);
+}
+
+}  // namespace oc

@@ -157,6 +157,43 @@ def test_large_m_kernel_one_hot_bit_exact(M, K, N, kind):
     assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, torch.bfloat16))
 
 
+@pytest.mark.parametrize("M,K,N,kind", [(1100, 1024, 200, "gs32_v1"), (1024, 2048, 400, "actorder"),
+                                         (1030, 1040, 96, "gs26"), (1500, 512, 1000, "gs128"),
+                                         (1024, 1024, 320, "fp16"), (1024, 512, 264, "bf16_scales"),
+                                         (4096, 256, 12288, "v2")])
+def test_wide_kernel_one_hot_bit_exact(M, K, N, kind):
+    """The 256-row wave-tile kernel (M >= 1024: 192- or 256-column blocks,
+    ragged M and N, gathered act-order rows, padded and wide groups, fp16
+    activations, bf16 scales) reproduces dequantized columns exactly."""
+    from onecomp_runtime import synthetic
+
+    kw = dict(seed=34)
+    dtype = torch.bfloat16
+    if kind == "v2":
+        kw["v1"] = False
+    if kind == "actorder":
+        kw["act_order"] = True
+    if kind == "gs26":
+        kw["groupsize"] = 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    if kind == "fp16":
+        dtype = torch.float16
+    if kind == "bf16_scales":
+        kw["scale_dtype"] = torch.bfloat16
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer, dtype)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16" if dtype == torch.bfloat16 else "f16", layer.v1)
+    rng = np.random.default_rng(6)
+    ks = rng.integers(0, K, M)
+    x = torch.zeros((M, K), dtype=dtype)
+    x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+    say(f"wide one-hot M={M} K={K} N={N} kind={kind}")
+    out = _gemm_raw(mod, x.to(DEV), TILED)
+    assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
+
+
 # -- regimes and shapes -------------------------------------------------------
 @pytest.mark.parametrize("M", [1, 3, 16, 17, 33, 64])
 def test_splitk_and_tiled_agree_with_oracle(M):
