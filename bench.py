@@ -70,6 +70,29 @@ def time_ms(launch, iters: int, warmup: int) -> float:
     return start.elapsed_time(end) / iters
 
 
+def graph_ms(calls, replays: int = 10) -> float:
+    """Average ms per call of ``calls`` (zero-argument launches, e.g. one per
+    weight copy) captured back to back into one HIP graph and replayed."""
+    import torch
+
+    for c in calls:  # eager once: workspaces reach their size before capture
+        c()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for c in calls:
+            c()
+    g.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(replays):
+        g.replay()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / (replays * len(calls))
+
+
 def build_gptq(K, N, *, seed, dev, copies, **kw):
     """One module per weight copy (distinct device memory), same values."""
     import torch
@@ -182,10 +205,11 @@ def gptq_m16_workload(dev, steps, warmup):
     _, mods = build_gptq(K, N, seed=20260, dev=dev, copies=copies)
     x = synthetic.activations(16, K, seed=20261).to(dev)
     with torch.no_grad():
-        ms = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+        ms_eager = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+        ms = graph_ms([lambda m=m: m(x) for m in mods])
     gbps = gptq_bytes(K, N) / (ms * 1e-3) / 1e9
     return {"M": 16, "K": K, "N": N, "us": ms * 1e3, "weight_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBS,
-            "TFLOPs": 2 * 16 * K * N / (ms * 1e-3) / 1e12}
+            "TFLOPs": 2 * 16 * K * N / (ms * 1e-3) / 1e12, "us_eager": ms_eager * 1e3}
 
 
 def dit_workload(dev, steps, warmup):
@@ -200,7 +224,7 @@ def dit_workload(dev, steps, warmup):
         _, mods = build_gptq(K, N, seed=20280 + i, dev=dev, copies=1, v1=False)
         x = synthetic.activations(4096, K, seed=20281, outliers=True).to(dev)
         with torch.no_grad():
-            ms = time_ms(lambda j: mods[0](x), steps, warmup)
+            ms = graph_ms([lambda: mods[0](x)] * 4, replays=max(3, steps // 4))
             # Context only: a dense bf16 GEMM of the same shape on an already
             # dequantized weight, as the vendor library (hipBLASLt) runs it.
             wd = torch.randn(N, K, dtype=torch.bfloat16, device=dev)
@@ -227,11 +251,12 @@ def padded_workload(dev, steps, warmup):
     _, mods = build_gptq(K, N, seed=20290, dev=dev, copies=copies, groupsize=26, pad_rows_to=1056)
     x = synthetic.activations(M, K, seed=20291).to(dev)
     with torch.no_grad():
-        ms = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+        ms_eager = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
+        ms = graph_ms([lambda m=m: m(x) for m in mods])
     tf = 2 * M * K * N / (ms * 1e-3) / 1e12
     wb = 1056 // 8 * N * 4 + 40 * N * 2 + 40 * N // 8 * 4
     return {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
-            "GBps": (wb + M * K * 2 + M * N * 2) / (ms * 1e-3) / 1e9}
+            "GBps": (wb + M * K * 2 + M * N * 2) / (ms * 1e-3) / 1e9, "us_eager": ms_eager * 1e3}
 
 
 def rtn_workload(dev, steps, warmup):
@@ -245,9 +270,11 @@ def rtn_workload(dev, steps, warmup):
     mod = PackedRTNLinear(K, N, layer.qweight_u8.to(dev), layer.scales.to(dev), layer.zeros.to(dev))
     x = synthetic.activations(M, K, seed=20301).to(dev)
     with torch.no_grad():
-        ms = time_ms(lambda i: mod(x), steps * 4, warmup)
+        ms_eager = time_ms(lambda i: mod(x), steps * 4, warmup)
+        ms = graph_ms([lambda: mod(x)] * 8)
     tf = 2 * M * K * N / (ms * 1e-3) / 1e12
-    res["rtn_linear_m512"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS}
+    res["rtn_linear_m512"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
+                              "us_eager": ms_eager * 1e3}
     V, D, T = 32768, 1024, 4096
     for G in (1, 32):
         emb_layer = synthetic.rtn_layer(V, D, seed=20310, groups=G)
@@ -255,10 +282,12 @@ def rtn_workload(dev, steps, warmup):
                               emb_layer.zeros.to(dev))
         ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311)).to(dev)
         with torch.no_grad():
-            ms = time_ms(lambda i: emb(ids), steps * 4, warmup)
+            ms_eager = time_ms(lambda i: emb(ids), steps * 4, warmup)
+            ms = graph_ms([lambda: emb(ids)] * 8)
         nbytes = T * (D // 2 + 4 * G) + T * 8 + T * D * 2
         res[f"rtn_embedding_G{G}"] = {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
-                                      "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                                      "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                      "us_eager": ms_eager * 1e3}
     return res
 
 
@@ -281,11 +310,13 @@ def moe_workload(dev, steps, warmup):
         kernels.int4_moe_gemm(x, topk, w[i % copies], off, pairs)
 
     with torch.no_grad():
-        ms = time_ms(step, steps, warmup)
+        ms_eager = time_ms(step, steps, warmup)
+        ms = graph_ms([lambda c=c: step(c) for c in range(copies)] * 2)
     wbytes = E * gptq_bytes(K, N)
     flops = 2 * T * topk * K * N
     return {"us": ms * 1e3, "weight_GBps": wbytes / (ms * 1e-3) / 1e9,
-            "hbm_frac": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "TFLOPs": flops / (ms * 1e-3) / 1e12}
+            "hbm_frac": wbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, "TFLOPs": flops / (ms * 1e-3) / 1e12,
+            "us_eager": ms_eager * 1e3}
 
 
 def cpu_baseline(budget_s: float):

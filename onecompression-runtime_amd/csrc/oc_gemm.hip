@@ -55,47 +55,6 @@ constexpr int DOT_PF = 3;  // K steps in flight per lane
 // scattered to their physical positions through kinv (act-order / padded).
 enum { XS_CONTIG = 0, XS_SCATTER = 1 };
 
-template <int DT>
-__device__ __forceinline__ float dot2acc(uint32_t b, uint32_t x, float acc) {
-  if constexpr (DT == OC_DTYPE_BF16) {
-    return __builtin_amdgcn_fdot2_f32_bf16(bitcast<v2bf16>(b), bitcast<v2bf16>(x), acc, false);
-  } else {
-    return __builtin_amdgcn_fdot2(bitcast<v2f16>(b), bitcast<v2f16>(x), acc, false);
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ float half_to_f32(uint32_t h16) {
-  if constexpr (DT == OC_DTYPE_BF16) return bf16_to_f32(static_cast<uint16_t>(h16));
-  else return f16_to_f32(static_cast<uint16_t>(h16));
-}
-
-template <int DT>
-constexpr float dot_base() {
-  return DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
-}
-
-// Pair words of one octet given as 4 raw words {x0|x1<<16, x2|x3<<16, ...},
-// and the octet's sum (fp32, in row order).
-template <int DT>
-__device__ __forceinline__ uint4 octet_pairs(uint4 raw, float &sum) {
-  const uint32_t lo = 0x05040100u, hi = 0x07060302u;  // v_perm selectors: low / high halves of two words
-  uint4 r;
-  r.x = __builtin_amdgcn_perm(raw.z, raw.x, lo);  // x0 | x4 << 16
-  r.y = __builtin_amdgcn_perm(raw.z, raw.x, hi);  // x1 | x5 << 16
-  r.z = __builtin_amdgcn_perm(raw.w, raw.y, lo);  // x2 | x6 << 16
-  r.w = __builtin_amdgcn_perm(raw.w, raw.y, hi);  // x3 | x7 << 16
-  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    s += half_to_f32<DT>(w[i] & 0xFFFFu);
-    s += half_to_f32<DT>(w[i] >> 16);
-  }
-  sum = s;
-  return r;
-}
-
 __host__ __device__ inline int dot_ksp(int KS) { return (KS + 1) & ~1; }
 size_t dot_lds_bytes(int MR, int KS) {
   return static_cast<size_t>(MR) * (KS * 4 * sizeof(uint4) + dot_ksp(KS) * sizeof(float2));
@@ -970,7 +929,16 @@ struct Plan {
   int waves;     // decode kernel: launch shape (DOT_W*)
   bool big;      // large M: gemm_big_kernel
   int wide_wn;   // large M: gemm_wide_kernel with this many tiles per wave (0: not used)
+  bool legacy_dot;  // decode: whole-tile gemv_dot_kernel (else the split-item GEMV)
+  GemvPlan gv;      // decode: split GEMV work items
 };
+
+// Workspace layout, every regime: [counter area][gathered activations][fp32
+// partials]. The counter area holds the decode kernel's per-group arrival
+// counters; it must be zero when a workspace is first used and every call
+// leaves it zero, so no regime writes anything else there.
+constexpr size_t COUNTER_BYTES = 16384;
+constexpr int COUNTER_SLOTS = static_cast<int>(COUNTER_BYTES / sizeof(int));
 
 // Compute units of the current device (cached per device).
 int device_cus() {
@@ -988,20 +956,22 @@ int device_cus() {
 
 // Tiles per wave of the wide kernel for an M x N problem: the shape whose
 // workgroups fill the compute units best (whole waves of workgroups over the
-// CUs, times the useful fraction of the last column block); ties go to 4.
+// CUs, times the useful fraction of the last column block). Ties go to 3
+// tiles (192 columns), measured as fast as 4 on full grids and lighter on
+// registers.
 int pick_wide_wn(int M, int N) {
   static const int forced = env_int("ONECOMP_HIP_WIDE_WN", 0);
   if (forced == 3 || forced == 4) return forced;
   const int cus = device_cus();
   double best = -1.0;
-  int pick = 4;
-  for (int wn : {4, 3}) {
+  int pick = 3;
+  for (int wn : {3, 4}) {
     const int64_t nbn = (N + 64 * wn - 1) / (64 * wn), nbm = (M + 255) / 256;
     const int64_t blocks = nbn * nbm;
     const double fill = static_cast<double>(blocks) / (static_cast<double>((blocks + cus - 1) / cus) * cus);
     const double useful = static_cast<double>(N) / (static_cast<double>(nbn) * 64 * wn);
     const double score = fill * useful;
-    if (score > best + 1e-9) {
+    if (score > best + 0.02) {
       best = score;
       pick = wn;
     }
@@ -1012,8 +982,11 @@ int pick_wide_wn(int M, int N) {
 // The decode kernel takes M <= 2, power-of-two groups of 32-row steps and its
 // activation rows in (at most 128 KB of) LDS.
 bool dot_eligible(int M, int K_phys, int group_rows) {
-  return M >= 1 && M <= 2 && ilog2_exact(group_rows / 32) >= 0 && dot_lds_bytes(M, K_phys / 32) <= 128 * 1024;
+  (void)K_phys;
+  return M >= 1 && M <= 2 && ilog2_exact(group_rows / 32) >= 0;
 }
+// The whole-tile kernel stages the entire activation row in LDS.
+bool legacy_dot_fits(int M, int K_phys) { return dot_lds_bytes(M, K_phys / 32) <= 128 * 1024; }
 
 Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regime, bool has_kinv = true,
                int64_t lda_hint = 0) {
@@ -1023,7 +996,7 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   static const bool dot_disabled = env_int("ONECOMP_HIP_DISABLE_DOT", 0) != 0;
   static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
   if (regime == OC_REGIME_AUTO) {
-    if (!dot_disabled && (!has_kmap || has_kinv) && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
+    if (!dot_disabled && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
     else regime = M <= 64 ? OC_REGIME_SPLITK : OC_REGIME_TILED;
   }
   sp.regime = regime;
@@ -1031,6 +1004,22 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   sp.ksteps_per_split = ksteps;
   sp.gather = has_kmap && regime != OC_REGIME_DOT;
   if (regime == OC_REGIME_DOT) {
+    // Whole-tile kernel when it can run (measured faster or equal on the
+    // decode shapes); the split-item kernel (oc_gemv.hip) gathers through
+    // kmap without kinv and has no K limit. ONECOMP_HIP_GEMV_SPLIT=1 forces it.
+    static const bool split_forced = env_int("ONECOMP_HIP_GEMV_SPLIT", 0) != 0;
+    if (split_forced || (has_kmap && !has_kinv) || !legacy_dot_fits(M, K_phys)) {
+      // Balanced work items; K split when it evens the load.
+      sp.gv = plan_gemv(M, N, ksteps, has_kmap, device_cus());
+      const int tiles = (N + TILE_N - 1) / TILE_N;
+      if (sp.gv.ksplit > 1 && (tiles + sp.gv.T - 1) / sp.gv.T > COUNTER_SLOTS)
+        sp.gv = GemvPlan{sp.gv.T, (ksteps + 3) / 4 * 4, 1};
+      sp.ksplit = sp.gv.ksplit;
+      sp.ksteps_per_split = sp.gv.S;
+      sp.gather = false;
+      return sp;
+    }
+    sp.legacy_dot = true;
     static const int dot_shape = env_int("ONECOMP_HIP_DOT_SHAPE", -1);
     // 8 waves; half tiles (twice the workgroups) for narrow layers (N < 2048;
     // wider ones measured faster with whole tiles, which stage activations once
@@ -1091,7 +1080,7 @@ size_t gather_bytes(const Plan &sp, int M, int K_phys) {
 size_t workspace_bytes(const Plan &sp, int M, int N, int K_phys) {
   size_t b = gather_bytes(sp, M, K_phys);
   if (sp.ksplit > 1) b += static_cast<size_t>(sp.ksplit) * M * N * sizeof(float);
-  return b;
+  return b > 0 ? COUNTER_BYTES + b : 0;
 }
 
 template <int DT, int SDT, int MR, int XS, int WAVES, int CPW>
@@ -1243,18 +1232,14 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
     return fail(OC_ERR_SHAPE, "activations need 16-byte aligned rows (lda %% 8 == 0)");
   if (!aligned(qt, 16) || !aligned(kmap, 16) || !aligned(kinv, 16))
     return fail(OC_ERR_SHAPE, "qweight, kmap and kinv must be 16-byte aligned");
-  if (regime == OC_REGIME_DOT && kmap && !kinv)
-    return fail(OC_ERR_INVALID_ARGUMENT, "the decode regime needs kinv with kmap");
   const int64_t tiles = (N + TILE_N - 1) / TILE_N;
   if (tiles * (K_phys / 32) * 64 >= (1LL << 31))
     return fail(OC_ERR_UNSUPPORTED, "layer too large for 32-bit tile offsets");
   if (regime == OC_REGIME_SPLITK && M > 64)
     return fail(OC_ERR_UNSUPPORTED, "small-M regime supports M <= 64, got M=%d", M);
   if (regime == OC_REGIME_DOT && !dot_eligible(M, K_phys, group_rows))
-    return fail(OC_ERR_UNSUPPORTED,
-                "decode regime needs M <= 2, group_rows/32 a power of two and M*K_phys*2.25 B of LDS <= 128 KB "
-                "(M=%d K_phys=%d group_rows=%d)",
-                M, K_phys, group_rows);
+    return fail(OC_ERR_UNSUPPORTED, "decode regime needs M <= 2 and group_rows/32 a power of two (M=%d group_rows=%d)",
+                M, group_rows);
 
   const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime, kinv != nullptr, lda);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
@@ -1286,16 +1271,19 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.ldc = ldc;
   p.ksplit = sp.ksplit;
   p.ksteps_per_split = sp.ksteps_per_split;
+  char *ws_after_counters = need > 0 ? static_cast<char *>(workspace) + COUNTER_BYTES : nullptr;
   if (sp.gather) {
-    launch_gather_cols(a, lda, M, K_logical, kmap, kinv, K_phys, workspace, stream);
-    p.a = workspace;
+    launch_gather_cols(a, lda, M, K_logical, kmap, kinv, K_phys, ws_after_counters, stream);
+    p.a = ws_after_counters;
     p.lda = K_phys;
   }
   p.a_bytes = (static_cast<int64_t>(M) - 1) * p.lda * 2 + static_cast<int64_t>(sp.gather ? K_phys : K_logical) * 2;
-  if (sp.ksplit > 1)
-    p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + gather_bytes(sp, M, K_phys));
+  if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(ws_after_counters + gather_bytes(sp, M, K_phys));
+  p.kmap = kmap;
+  p.counters = need > 0 ? static_cast<int *>(workspace) : nullptr;
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (sp.wide_wn) launch_gptq_wide(p, a_dtype, scale_dtype, sp.wide_wn, s);
+  if (sp.regime == OC_REGIME_DOT && !sp.legacy_dot) launch_gptq_gemv(p, a_dtype, scale_dtype, sp.gv.T, s);
+  else if (sp.wide_wn) launch_gptq_wide(p, a_dtype, scale_dtype, sp.wide_wn, s);
   else if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);
   else if (bf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_F16>(p, sp, s);
   else if (sbf) launch_gptq<OC_DTYPE_F16, OC_DTYPE_BF16>(p, sp, s);

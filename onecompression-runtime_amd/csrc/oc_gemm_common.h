@@ -50,6 +50,9 @@ struct GemmParams {
   int64_t qw_expert_stride;  // 32-bit words per expert
   int64_t s_expert_stride;   // 16-bit scales per expert
   int64_t z_expert_stride;   // zero words per expert
+  // decode (split GEMV)
+  const int32_t *kmap;  // physical -> logical row (-1: padding), NULL: identity
+  int *counters;        // per tile group arrival counters (zero between calls)
 };
 
 __device__ __forceinline__ int group_of(const GemmParams &p, int ks) {
@@ -114,11 +117,68 @@ using ic = std::integral_constant<int, I>;
 // or 16 lanes the LDS serves together (32 or 64 banks of 4 bytes).
 __device__ __forceinline__ int big_swz(int r) { return ((r >> 1) ^ (r >> 2)) & 3; }
 
+// ---- decode inner-product helpers (x-pair staging) ----
+
+template <int DT>
+__device__ __forceinline__ float dot2acc(uint32_t b, uint32_t x, float acc) {
+  if constexpr (DT == OC_DTYPE_BF16) {
+    return __builtin_amdgcn_fdot2_f32_bf16(bitcast<v2bf16>(b), bitcast<v2bf16>(x), acc, false);
+  } else {
+    return __builtin_amdgcn_fdot2(bitcast<v2f16>(b), bitcast<v2f16>(x), acc, false);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ float half_to_f32(uint32_t h16) {
+  if constexpr (DT == OC_DTYPE_BF16) return bf16_to_f32(static_cast<uint16_t>(h16));
+  else return f16_to_f32(static_cast<uint16_t>(h16));
+}
+
+template <int DT>
+constexpr float dot_base() {
+  return DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
+}
+
+// Pair words of one octet given as 4 raw words {x0|x1<<16, x2|x3<<16, ...},
+// and the octet's sum (fp32, in row order).
+template <int DT>
+__device__ __forceinline__ uint4 octet_pairs(uint4 raw, float &sum) {
+  const uint32_t lo = 0x05040100u, hi = 0x07060302u;  // v_perm selectors: low / high halves of two words
+  uint4 r;
+  r.x = __builtin_amdgcn_perm(raw.z, raw.x, lo);  // x0 | x4 << 16
+  r.y = __builtin_amdgcn_perm(raw.z, raw.x, hi);  // x1 | x5 << 16
+  r.z = __builtin_amdgcn_perm(raw.w, raw.y, lo);  // x2 | x6 << 16
+  r.w = __builtin_amdgcn_perm(raw.w, raw.y, hi);  // x3 | x7 << 16
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s += half_to_f32<DT>(w[i] & 0xFFFFu);
+    s += half_to_f32<DT>(w[i] >> 16);
+  }
+  sum = s;
+  return r;
+}
+
+
 // Host helpers.
 int env_int(const char *name, int dflt);
 
 // Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
 // ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);
+
+// Decode GEMV over work items of T tiles x S K steps (oc_gemv.hip). K is split
+// into ksplit = ceil(KS / S) ranges; with ksplit > 1 the launch needs
+// p.partials (ksplit * M * N floats) and p.counters (one zeroed int per
+// group of T tiles, left zero).
+struct GemvPlan {
+  int T;       // tiles per item
+  int S;       // K steps per item
+  int ksplit;  // K ranges
+};
+GemvPlan plan_gemv(int M, int N, int KS, bool gather, int cus);
+size_t gemv_lds_bytes(int MR, int S);
+void launch_gptq_gemv(const GemmParams &p, int a_dtype, int scale_dtype, int T, hipStream_t s);
 
 }  // namespace oc

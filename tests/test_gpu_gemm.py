@@ -414,18 +414,102 @@ def test_decode_kernel_ragged_k(K, N, gs, act, M):
     assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"ragged dot K={K}")
 
 
-def test_decode_regime_needs_kinv():
+def test_decode_regime_gathers_through_kmap():
+    """The decode kernel gathers act-order activations through kmap itself:
+    kinv is optional, and with or without it the result is the same."""
     from onecomp_runtime import kernels, synthetic
 
     layer = synthetic.gptq_layer(1024, 64, seed=78, act_order=True)
     mod = _module_for(layer)
     x = synthetic.activations(1, 1024, seed=79).to(DEV)
     say("decode without kinv")
-    with pytest.raises(ValueError):
-        kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, regime=DOT)
-    # AUTO then takes the small-M MFMA path on gathered activations
-    out = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap)
-    assert_gemm_close(out, _oracle_out(layer, x.cpu()), "auto without kinv")
+    out = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, regime=DOT)
+    assert_gemm_close(out, _oracle_out(layer, x.cpu()), "decode without kinv")
+    with_kinv = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, kinv=mod.kinv, regime=DOT)
+    assert_gemm_close(with_kinv, _oracle_out(layer, x.cpu()), "decode with kinv")
+    auto = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap)
+    assert torch.equal(out, auto)
+
+
+# -- split-item decode kernel (act-order without kinv; K beyond the LDS of the
+# whole-tile kernel): K split over workgroups, partials summed in split order by
+# the last workgroup of each tile group (device-scope counters that reset). ---
+def _split_gemv(mod, x, bias=None):
+    from onecomp_runtime import kernels
+
+    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, bias=bias, regime=DOT)
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (17408, 5120), (5120, 1024), (1040, 200), (2048, 17408)])
+@pytest.mark.parametrize("M", [1, 2])
+def test_split_gemv_matches_oracle(K, N, M):
+    from onecomp_runtime import synthetic
+
+    kw = dict(seed=90 + K + M, act_order=True)
+    if K == 1040:
+        kw = dict(seed=91, groupsize=26)  # padded groups: kmap holds -1 rows
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer)
+    x = synthetic.activations(M, K, seed=92)
+    say(f"split gemv K={K} N={N} M={M}")
+    assert_gemm_close(_split_gemv(mod, x.to(DEV)), _oracle_out(layer, x), f"split gemv K={K} N={N} M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_split_gemv_one_hot_bit_exact(M):
+    from onecomp_runtime import synthetic
+
+    K, N = 4096, 320
+    layer = synthetic.gptq_layer(K, N, seed=93, act_order=True)
+    mod = _module_for(layer)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16", layer.v1)
+    rng = np.random.default_rng(2)
+    for rep in range(3):
+        ks = rng.choice(K, M, replace=False)
+        x = torch.zeros((M, K), dtype=torch.bfloat16)
+        x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+        say(f"split gemv one-hot M={M} rep={rep}")
+        assert np.array_equal(bits16(_split_gemv(mod, x.to(DEV))), oracle_bits(wd[:, ks].T, torch.bfloat16))
+
+
+def test_split_gemv_bias_fp16_deterministic_and_graph():
+    from onecomp_runtime import synthetic
+
+    K, N = 8192, 1024
+    layer = synthetic.gptq_layer(K, N, seed=94, act_order=True)
+    mod16 = _module_for(layer, torch.float16)
+    x = synthetic.activations(1, K, seed=95, dtype=torch.float16)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(96)).to(torch.float16)
+    say("split gemv fp16 + bias")
+    out = _split_gemv(mod16, x.to(DEV), bias.to(DEV))
+    assert_gemm_close(out, _oracle_out(layer, x, "f16", bias), "split gemv fp16 bias")
+    for rep in range(5):
+        assert torch.equal(_split_gemv(mod16, x.to(DEV), bias.to(DEV)), out), f"rep {rep} differs"
+    # Graph replays reuse the counters: each replay must match the eager result.
+    xd, bd = x.to(DEV), bias.to(DEV)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = _split_gemv(mod16, xd, bd)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, out), f"graph replay {rep} differs"
+        assert torch.equal(_split_gemv(mod16, xd, bd), out)
+
+
+def test_split_gemv_beyond_whole_tile_lds():
+    """K = 65536 does not fit the whole-tile kernel's activation staging: the
+    split kernel takes it, also without act-order."""
+    from onecomp_runtime import synthetic
+
+    K, N = 65536, 96
+    layer = synthetic.gptq_layer(K, N, seed=97)
+    mod = _module_for(layer)
+    x = synthetic.activations(1, K, seed=98)
+    say("split gemv K=65536")
+    out = mod(x.to(DEV))
+    assert_gemm_close(out, _oracle_out(layer, x), "split gemv K=65536")
 
 
 @pytest.mark.parametrize("regime", [DOT, SPLITK, TILED])
