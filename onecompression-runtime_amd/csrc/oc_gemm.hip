@@ -49,7 +49,7 @@ namespace oc {
 // scatter each value to its physical row through kinv (logical -> physical),
 // so every global access of the staging stays coalesced; a per-workgroup
 // gather through kmap would touch one cache line per lane.
-constexpr int DOT_PF = 3;  // K steps in flight per lane
+constexpr int DOT_PF = 2;  // K steps in flight per lane (measured: 2 beats 3-5; fewer registers, more waves)
 
 // How the decode kernel stages its activations: contiguous rows, or rows
 // scattered to their physical positions through kinv (act-order / padded).
@@ -631,23 +631,28 @@ struct BigLayout {
 };
 
 
-template <int DT, int SDT, int WM, int WN, int KPS, bool MOE>
-__global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
+template <int DT, int SDT, int WM, int WN, int KPS, bool MOE, int NSX = (KPS == 1 ? 4 : 3)>
+__global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
   // WM 16-row tiles per workgroup; KPS K steps per ring stage (one barrier
   // per stage); ring depth NS. MOE: grid z = expert; the workgroup walks its
   // expert's routed rows (expert_offsets / sorted_pairs) in blocks of 16 WM.
   using L = BigLayout<WN>;
   constexpr int BM = 16 * WM;
-  constexpr int NS = KPS == 1 ? 4 : 3;
+  constexpr int NS = NSX;  // ring depth: NS - 1 stages in flight
+  static_assert(NS >= 3 && NS <= 8, "ring depth");
   constexpr int TILES = L::TILES;
   constexpr int AST = BM * 4;       // uint4 per K step of activations
   constexpr int ADMA = BM / 64;     // activation DMAs per wave per K step
   constexpr int DMA = ADMA + L::WDMA;
   static_assert((WM == 4 || WM == 8 || WM == 16) && (WN == 3 || WN == 6) && (KPS == 1 || KPS == 2),
                 "DMA assignment");
-  __shared__ __attribute__((aligned(1024))) uint4 A0[KPS * AST], A1[KPS * AST], A2[KPS * AST], A3[NS == 4 ? KPS * AST : 1];
-  __shared__ __attribute__((aligned(1024))) uint32_t W0[KPS * L::DW], W1[KPS * L::DW], W2[KPS * L::DW],
-      W3[NS == 4 ? KPS * L::DW : 1];
+  // One distinct LDS array per ring slot (the compiler's wait insertion tells
+  // DMA targets apart by array); slots past NS are one element.
+  constexpr int ASZ = KPS * AST, WSZ = KPS * L::DW;
+  __shared__ __attribute__((aligned(1024))) uint4 A0[ASZ], A1[ASZ], A2[ASZ], A3[NS > 3 ? ASZ : 1],
+      A4[NS > 4 ? ASZ : 1], A5[NS > 5 ? ASZ : 1], A6[NS > 6 ? ASZ : 1], A7[NS > 7 ? ASZ : 1];
+  __shared__ __attribute__((aligned(1024))) uint32_t W0[WSZ], W1[WSZ], W2[WSZ], W3[NS > 3 ? WSZ : 1],
+      W4[NS > 4 ? WSZ : 1], W5[NS > 5 ? WSZ : 1], W6[NS > 6 ? WSZ : 1], W7[NS > 7 ? WSZ : 1];
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
@@ -757,13 +762,35 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
     };
 
     // One ring stage on slot U (a compile-time constant).
+    auto slot_a = [&](auto U) -> uint4 * {
+      constexpr int u = decltype(U)::value;
+      if constexpr (u == 0) return A0;
+      else if constexpr (u == 1) return A1;
+      else if constexpr (u == 2) return A2;
+      else if constexpr (u == 3) return A3;
+      else if constexpr (u == 4) return A4;
+      else if constexpr (u == 5) return A5;
+      else if constexpr (u == 6) return A6;
+      else return A7;
+    };
+    auto slot_w = [&](auto U) -> uint32_t * {
+      constexpr int u = decltype(U)::value;
+      if constexpr (u == 0) return W0;
+      else if constexpr (u == 1) return W1;
+      else if constexpr (u == 2) return W2;
+      else if constexpr (u == 3) return W3;
+      else if constexpr (u == 4) return W4;
+      else if constexpr (u == 5) return W5;
+      else if constexpr (u == 6) return W6;
+      else return W7;
+    };
     auto step = [&](auto U, int stage) {
       constexpr int u = decltype(U)::value;
       constexpr int un = (u + NS - 1) % NS;
-      uint4 *ab = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
-      uint32_t *wb = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
-      uint4 *abn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
-      uint32_t *wbn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
+      uint4 *ab = slot_a(U);
+      uint32_t *wb = slot_w(U);
+      uint4 *abn = slot_a(ic<un>{});
+      uint32_t *wbn = slot_w(ic<un>{});
       wait_vmcnt<DMA * KPS * (NS - 2)>();  // this wave's copies of the stage landed ...
       barrier_no_fence();                      // ... and everyone's; slot un is free again
       issue(abn, wbn, stage + NS - 1);
@@ -771,34 +798,29 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 ? 2 : 1) void gemm_big_kern
       for (int h = 0; h < KPS; ++h)
         if (ks_begin + KPS * stage + h < ks_end) compute1(ab + h * AST, wb + h * L::DW);
     };
+    // Ring cycle starting at stage s0 over slots 0 .. n-1 (n <= NS).
+    auto cycle = [&](int s0, int n) {
+      if (n > 0) step(ic<0>{}, s0);
+      if (n > 1) step(ic<1>{}, s0 + 1);
+      if (n > 2) step(ic<2>{}, s0 + 2);
+      if constexpr (NS > 3) if (n > 3) step(ic<3>{}, s0 + 3);
+      if constexpr (NS > 4) if (n > 4) step(ic<4>{}, s0 + 4);
+      if constexpr (NS > 5) if (n > 5) step(ic<5>{}, s0 + 5);
+      if constexpr (NS > 6) if (n > 6) step(ic<6>{}, s0 + 6);
+      if constexpr (NS > 7) if (n > 7) step(ic<7>{}, s0 + 7);
+    };
 
     issue(A0, W0, 0);
     issue(A1, W1, 1);
-    if constexpr (NS == 4) issue(A2, W2, 2);
+    if constexpr (NS > 3) issue(A2, W2, 2);
+    if constexpr (NS > 4) issue(A3, W3, 3);
+    if constexpr (NS > 5) issue(A4, W4, 4);
+    if constexpr (NS > 6) issue(A5, W5, 5);
+    if constexpr (NS > 7) issue(A6, W6, 6);
     const int nst = (ks_end - ks_begin + KPS - 1) / KPS;  // stages
-    if constexpr (NS == 4) {
-      const int nfull = nst / 4 * 4;
-      for (int s0 = 0; s0 < nfull; s0 += 4) {
-        step(ic<0>{}, s0);
-        step(ic<1>{}, s0 + 1);
-        step(ic<2>{}, s0 + 2);
-        step(ic<3>{}, s0 + 3);
-      }
-      const int rem = nst - nfull;
-      if (rem > 0) step(ic<0>{}, nfull);
-      if (rem > 1) step(ic<1>{}, nfull + 1);
-      if (rem > 2) step(ic<2>{}, nfull + 2);
-    } else {
-      const int nfull = nst / 3 * 3;
-      for (int s0 = 0; s0 < nfull; s0 += 3) {
-        step(ic<0>{}, s0);
-        step(ic<1>{}, s0 + 1);
-        step(ic<2>{}, s0 + 2);
-      }
-      const int rem = nst - nfull;
-      if (rem > 0) step(ic<0>{}, nfull);
-      if (rem > 1) step(ic<1>{}, nfull + 1);
-    }
+    const int nfull = nst / NS * NS;
+    for (int s0 = 0; s0 < nfull; s0 += NS) cycle(s0, NS);
+    if (nst > nfull) cycle(nfull, nst - nfull);
     wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
 
     // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
@@ -1048,8 +1070,9 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     // Pipelined 128 x 192 kernel; split K only when the grid cannot fill the chip.
     sp.big = true;
     const int blocks = ((M + 127) / 128) * ((N + 191) / 192);
+    static const int min_steps = std::max(1, env_int("ONECOMP_HIP_SPLIT_MIN_STEPS", 16));
     int ksplit = 1;
-    if (blocks < want) ksplit = std::min((want + blocks - 1) / blocks, std::max(1, ksteps / 16));
+    if (blocks < want) ksplit = std::min((want + blocks - 1) / blocks, std::max(1, ksteps / min_steps));
     sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
     sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
     return sp;
@@ -1171,6 +1194,17 @@ constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 1;
 // Grouped experts use the same 128-row blocks: measured faster than 64-row
 // blocks, whose experts with more than 64 routed rows stream their weights twice.
 constexpr int MOE_WM = BIG_WM;
+// Ring depth of the grouped launch: 4, as the dense one (measured on the
+// 64-expert top-8 workload: 6 stages no faster, 8 slower with one workgroup
+// per CU). ONECOMP_HIP_MOE_NS (4, 6 or 8) overrides (tuning only).
+constexpr int MOE_NS = 4;
+
+template <int DT, int SDT>
+void launch_moe(const GemmParams &p, dim3 grid, int ns, hipStream_t s) {
+  if (ns == 4) hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, MOE_WM, BIG_WN, BIG_KPS, true, 4>), grid, dim3(256), 0, s, p);
+  else if (ns == 6) hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, MOE_WM, BIG_WN, BIG_KPS, true, 6>), grid, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, MOE_WM, BIG_WN, BIG_KPS, true, 8>), grid, dim3(256), 0, s, p);
+}
 
 template <int DT, int SDT>
 void launch_big(const GemmParams &p, hipStream_t s) {
@@ -1415,14 +1449,11 @@ int oc_int4_moe_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t T, int
   const dim3 grid((N + 64 * BIG_WN - 1) / (64 * BIG_WN), 1, E);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = x_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf && sbf)
-    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_BF16, OC_DTYPE_BF16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
-  else if (bf)
-    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_BF16, OC_DTYPE_F16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
-  else if (sbf)
-    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_F16, OC_DTYPE_BF16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
-  else
-    hipLaunchKernelGGL((gemm_big_kernel<OC_DTYPE_F16, OC_DTYPE_F16, MOE_WM, BIG_WN, BIG_KPS, true>), grid, dim3(256), 0, s, p);
+  static const int moe_ns = env_int("ONECOMP_HIP_MOE_NS", MOE_NS);
+  if (bf && sbf) launch_moe<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, grid, moe_ns, s);
+  else if (bf) launch_moe<OC_DTYPE_BF16, OC_DTYPE_F16>(p, grid, moe_ns, s);
+  else if (sbf) launch_moe<OC_DTYPE_F16, OC_DTYPE_BF16>(p, grid, moe_ns, s);
+  else launch_moe<OC_DTYPE_F16, OC_DTYPE_F16>(p, grid, moe_ns, s);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
