@@ -168,17 +168,19 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  *   kmap     NULL or int32 [K_phys] (device, 16-byte aligned)
  *   kinv     NULL or uint16 [K_logical] (device, 16-byte aligned), the
  *            inverse of kmap: kinv[kmap[k']] = k'. Activations are permuted
- *            through it (coalesced) when given; the decode regime needs it
- *            whenever kmap is given (OC_REGIME_AUTO picks another regime
- *            without it).
+ *            through it (coalesced) when given; without it the decode regime
+ *            gathers through kmap (its split-item kernel).
  *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
  *   c        [M, N] (row stride ldc elements) of a_dtype
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
  * K_phys % group_rows == 0; without kmap K_logical == K_phys.
- * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned, any
- * contents) holds gathered activations (kmap with M > 2) and fp32 split-K
- * partials (large M, few output tiles); calls that overlap in time must not
- * share a workspace. `regime`: OC_REGIME_*.
+ * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned) starts
+ * with a 16 KB counter area, then holds gathered activations (kmap with M > 2)
+ * and fp32 split-K partials (large M with few output tiles, or a decode call
+ * whose K is split over workgroups). The counter area must hold zeros the
+ * first time a workspace is used (e.g. allocate it zero-filled) and every
+ * call leaves it zero again; the rest may hold anything. Calls that overlap
+ * in time must not share a workspace. `regime`: OC_REGIME_*.
  */
 int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
                  int32_t K_logical, const int32_t *qt, const void *st,
