@@ -685,6 +685,8 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void g
 
   // One block of up to BM rows starting at m0 (all waves, whole K range).
   auto run = [&](int m0) {
+    // Row tiles of this block holding rows (all of them unless grouped).
+    const int active_tiles = MOE ? min(WM, (row_end - m0 + 15) / 16) : WM;
     // Activation sources: DMA i of wave w fills LDS rows 16 (ADMA w + i) + lane / 4,
     // 16-byte position lane % 4, which holds chunk (position ^ big_swz(row)) of
     // that row (rows past the end re-read the last row; never stored).
@@ -754,6 +756,9 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void g
       }
 #pragma unroll
       for (int t = 0; t < WM; ++t) {
+        // Grouped experts fill a block only partly (~64 of 128 routed rows):
+        // row tiles past the expert's rows are skipped (a wave-uniform branch).
+        if (MOE && t >= active_tiles) break;
         const int row = 16 * t + c16;
         const uint4 av = ab[row * 4 + (quad ^ big_swz(row))];
 #pragma unroll

@@ -29,7 +29,7 @@
 
 namespace oc {
 
-constexpr int WIDE_NS = 4;  // LDS ring depth (stages)
+constexpr int WIDE_NS = 4;  // LDS ring depth (stages), default
 
 // One weight/metadata ring slot, in dwords.
 //   W: 4*WN tiles x 64 words (tile-major, as in global memory)
@@ -57,16 +57,38 @@ struct WideLayout {
 // voffset + OOB_OFFSET stays below 2^32 because every voffset is below 2^31.
 constexpr uint32_t OOB_OFFSET = 0x80000000u;
 
-template <int DT, int SDT, int WN>
+template <int DT, int SDT, int WN, int NS>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   using L = WideLayout<WN>;
-  constexpr int NS = WIDE_NS;
+  static_assert(NS == 4 || NS == 6, "ring depth");
   constexpr int BM = 256;
   constexpr int AST = BM * 4;  // uint4 per activation slot
   constexpr int DMA = 6;       // DMA instructions per wave and stage
   static_assert(NS % 2 == 0, "register sets alternate with the ring slots");
-  __shared__ __attribute__((aligned(1024))) uint4 A0[AST], A1[AST], A2[AST], A3[AST];
-  __shared__ __attribute__((aligned(1024))) uint32_t W0[L::DW], W1[L::DW], W2[L::DW], W3[L::DW];
+  // One distinct LDS array per ring slot (the compiler's wait insertion tells
+  // DMA targets apart by array); slots past NS are one element.
+  __shared__ __attribute__((aligned(1024))) uint4 A0[AST], A1[AST], A2[AST], A3[AST], A4[NS > 4 ? AST : 1],
+      A5[NS > 5 ? AST : 1];
+  __shared__ __attribute__((aligned(1024))) uint32_t W0[L::DW], W1[L::DW], W2[L::DW], W3[L::DW],
+      W4[NS > 4 ? L::DW : 1], W5[NS > 5 ? L::DW : 1];
+  auto slot_a = [&](auto U) -> uint4 * {
+    constexpr int u = decltype(U)::value;
+    if constexpr (u == 0) return A0;
+    else if constexpr (u == 1) return A1;
+    else if constexpr (u == 2) return A2;
+    else if constexpr (u == 3) return A3;
+    else if constexpr (u == 4) return A4;
+    else return A5;
+  };
+  auto slot_w = [&](auto U) -> uint32_t * {
+    constexpr int u = decltype(U)::value;
+    if constexpr (u == 0) return W0;
+    else if constexpr (u == 1) return W1;
+    else if constexpr (u == 2) return W2;
+    else if constexpr (u == 3) return W3;
+    else if constexpr (u == 4) return W4;
+    else return W5;
+  };
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -191,10 +213,10 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   auto step = [&](auto U, int s) {
     constexpr int u = decltype(U)::value;
     constexpr int un = (u + 1) % NS;
-    uint4 *as = u == 0 ? A0 : u == 1 ? A1 : u == 2 ? A2 : A3;
-    uint32_t *ws = u == 0 ? W0 : u == 1 ? W1 : u == 2 ? W2 : W3;
-    const uint4 *asn = un == 0 ? A0 : un == 1 ? A1 : un == 2 ? A2 : A3;
-    const uint32_t *wsn = un == 0 ? W0 : un == 1 ? W1 : un == 2 ? W2 : W3;
+    uint4 *as = slot_a(U);
+    uint32_t *ws = slot_w(U);
+    const uint4 *asn = slot_a(ic<un>{});
+    const uint32_t *wsn = slot_w(ic<un>{});
     uint4 *bc = u % 2 == 0 ? b0 : b1;
     uint4 *bn = u % 2 == 0 ? b1 : b0;
     wait_vmcnt<DMA * (NS - 2)>();  // this wave's copies of stage s + 1 landed ...
@@ -247,6 +269,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   issue(A1, W1, 1);
   issue(A2, W2, 2);
   issue(A3, W3, 3);
+  if constexpr (NS > 4) issue(A4, W4, 4);
+  if constexpr (NS > 5) issue(A5, W5, 5);
   wait_vmcnt<DMA * (NS - 1)>();
   barrier_no_fence();
   {
@@ -263,6 +287,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     step(ic<1>{}, s0 + 1);
     step(ic<2>{}, s0 + 2);
     step(ic<3>{}, s0 + 3);
+    if constexpr (NS > 4) step(ic<4>{}, s0 + 4);
+    if constexpr (NS > 5) step(ic<5>{}, s0 + 5);
   }
   wait_vmcnt<0>();  // no DMA outlives the workgroup's LDS
 
@@ -297,8 +323,11 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
 
 template <int DT, int SDT, int WN>
 static void launch_wide_t(const GemmParams &p, hipStream_t s) {
+  // ONECOMP_HIP_WIDE_NS = 6 selects the 6-slot ring (tuning only).
+  static const int ns = env_int("ONECOMP_HIP_WIDE_NS", WIDE_NS);
   const int nbn = (p.N + 64 * WN - 1) / (64 * WN), nbm = (p.M + 255) / 256;
-  hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN>), dim3(nbn * nbm), dim3(256), 0, s, p);
+  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 6>), dim3(nbn * nbm), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 4>), dim3(nbn * nbm), dim3(256), 0, s, p);
 }
 
 template <int DT, int SDT>
