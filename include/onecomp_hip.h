@@ -175,9 +175,11 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
  * K_phys % group_rows == 0; without kmap K_logical == K_phys.
  * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned) starts
- * with a 16 KB counter area, then holds gathered activations (kmap with M > 2)
- * and fp32 split-K partials (large M with few output tiles, or a decode call
- * whose K is split over workgroups). The counter area must hold zeros the
+ * with a 128 KB counter area (decode calls: arrival counters and the 64-bit
+ * cells through which two workgroups sharing an output tile exchange their
+ * partial sums), then holds gathered activations (kmap with M > 2) and fp32
+ * split-K partials (large M with few output tiles, or a decode call whose K
+ * is split over workgroups). The counter area must hold zeros the
  * first time a workspace is used (e.g. allocate it zero-filled) and every
  * call leaves it zero again; the rest may hold anything. Calls that overlap
  * in time must not share a workspace. `regime`: OC_REGIME_*.

@@ -60,11 +60,6 @@ size_t dot_lds_bytes(int MR, int KS) {
   return static_cast<size_t>(MR) * (KS * 4 * sizeof(uint4) + dot_ksp(KS) * sizeof(float2));
 }
 
-// Physical row r of activation row m -> its 16-bit slot in the x-pair block.
-__device__ __forceinline__ int xpair_slot(int m, int K_phys, int r) {
-  return m * K_phys + (r & ~7) + ((r & 3) << 1) + ((r >> 2) & 1);
-}
-
 template <int DT, int SDT, int MR, int XS, int WAVES, int CPW>
 __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
   // CPW columns per workgroup: a whole tile (16) or half of one (8; each K
@@ -958,13 +953,14 @@ struct Plan {
   int wide_wn;   // large M: gemm_wide_kernel with this many tiles per wave (0: not used)
   bool legacy_dot;  // decode: whole-tile gemv_dot_kernel (else the split-item GEMV)
   GemvPlan gv;      // decode: split GEMV work items
+  int stream_wgs;   // decode: balanced-range GEMV with this many workgroups (0: not used)
 };
 
 // Workspace layout, every regime: [counter area][gathered activations][fp32
-// partials]. The counter area holds the decode kernel's per-group arrival
-// counters; it must be zero when a workspace is first used and every call
+// partials]. The counter area holds the decode kernels' arrival counters and
+// swap cells; it must be zero when a workspace is first used and every call
 // leaves it zero, so no regime writes anything else there.
-constexpr size_t COUNTER_BYTES = 16384;
+constexpr size_t COUNTER_BYTES = 128 * 1024;
 constexpr int COUNTER_SLOTS = static_cast<int>(COUNTER_BYTES / sizeof(int));
 
 // Compute units of the current device (cached per device).
@@ -1031,10 +1027,19 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   sp.ksteps_per_split = ksteps;
   sp.gather = has_kmap && regime != OC_REGIME_DOT;
   if (regime == OC_REGIME_DOT) {
+    // Balanced-range kernel (oc_gemv_stream.hip) for layers of one to six
+    // tiles per compute unit whose activation rows fit in LDS: equal weight
+    // bytes per compute unit and one staging each (measured 8-18 % faster
+    // than whole tiles on 320 and 1088 tiles; a tie on 320 tiles of K=5120).
+    // ONECOMP_HIP_GEMV_STREAM=0 (read per call) selects the kernels below.
+    if (env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
+      sp.stream_wgs = gemv_stream_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
+      if (sp.stream_wgs > 0) return sp;
+    }
     // Whole-tile kernel when it can run (measured faster or equal on the
     // decode shapes); the split-item kernel (oc_gemv.hip) gathers through
     // kmap without kinv and has no K limit. ONECOMP_HIP_GEMV_SPLIT=1 forces it.
-    static const bool split_forced = env_int("ONECOMP_HIP_GEMV_SPLIT", 0) != 0;
+    const bool split_forced = env_int("ONECOMP_HIP_GEMV_SPLIT", 0) != 0;  // read per call (tests switch it)
     if (split_forced || (has_kmap && !has_kinv) || !legacy_dot_fits(M, K_phys)) {
       // Balanced work items; K split when it evens the load.
       sp.gv = plan_gemv(M, N, ksteps, has_kmap, device_cus());
@@ -1108,7 +1113,7 @@ size_t gather_bytes(const Plan &sp, int M, int K_phys) {
 size_t workspace_bytes(const Plan &sp, int M, int N, int K_phys) {
   size_t b = gather_bytes(sp, M, K_phys);
   if (sp.ksplit > 1) b += static_cast<size_t>(sp.ksplit) * M * N * sizeof(float);
-  return b > 0 ? COUNTER_BYTES + b : 0;
+  return b > 0 || sp.stream_wgs > 0 ? COUNTER_BYTES + b : 0;
 }
 
 template <int DT, int SDT, int MR, int XS, int WAVES, int CPW>
@@ -1321,7 +1326,8 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.kmap = kmap;
   p.counters = need > 0 ? static_cast<int *>(workspace) : nullptr;
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (sp.regime == OC_REGIME_DOT && !sp.legacy_dot) launch_gptq_gemv(p, a_dtype, scale_dtype, sp.gv.T, s);
+  if (sp.stream_wgs > 0) launch_gptq_gemv_stream(p, a_dtype, scale_dtype, sp.stream_wgs, s);
+  else if (sp.regime == OC_REGIME_DOT && !sp.legacy_dot) launch_gptq_gemv(p, a_dtype, scale_dtype, sp.gv.T, s);
   else if (sp.wide_wn) launch_gptq_wide(p, a_dtype, scale_dtype, sp.wide_wn, s);
   else if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);
   else if (bf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_F16>(p, sp, s);

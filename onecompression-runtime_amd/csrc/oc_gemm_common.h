@@ -40,7 +40,7 @@ struct GemmParams {
   int bias_dtype;
   void *c;
   int64_t ldc;
-  float *partials;  // [ksplit, M, N] fp32 (large-M split-K only)
+  float *partials;  // fp32 partial sums [ksplit, M, N] (split-K)
   int ksplit;
   int ksteps_per_split;
   // grouped (MoE) launch
@@ -139,6 +139,12 @@ constexpr float dot_base() {
   return DT == OC_DTYPE_BF16 ? 128.f : 1024.f;
 }
 
+// Physical row r of activation row m -> its 16-bit slot in an x-pair block
+// (rows of K_phys values; octet pairs (i, i + 4) adjacent).
+__device__ __forceinline__ int xpair_slot(int m, int K_phys, int r) {
+  return m * K_phys + (r & ~7) + ((r & 3) << 1) + ((r >> 2) & 1);
+}
+
 // Pair words of one octet given as 4 raw words {x0|x1<<16, x2|x3<<16, ...},
 // and the octet's sum (fp32, in row order).
 template <int DT>
@@ -180,5 +186,13 @@ struct GemvPlan {
 GemvPlan plan_gemv(int M, int N, int KS, bool gather, int cus);
 size_t gemv_lds_bytes(int MR, int S);
 void launch_gptq_gemv(const GemmParams &p, int a_dtype, int scale_dtype, int T, hipStream_t s);
+
+// Decode GEMV with one balanced weight range per workgroup
+// (oc_gemv_stream.hip). gemv_stream_wgs gives the launch width for a layer
+// (0: not applicable: M > 2, activation rows beyond LDS, fewer tiles than
+// workgroups, or more swap cells than cell_bytes hold). The launch needs
+// p.counters: nwg * M * 16 zeroed 64-bit cells, left zero.
+int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
+void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s);
 
 }  // namespace oc

@@ -39,6 +39,22 @@ def _oracle_out(layer, x: torch.Tensor, dtype="bf16", bias=None):
                          bias=None if bias is None else np32(bias))
 
 
+@pytest.fixture
+def decode_kernel(monkeypatch):
+    """use(kind) selects the decode (M <= 2) kernel: "stream" (balanced weight
+    range per workgroup, the default), "tile" (one 16-column tile per
+    workgroup) or "split" (K-split work items)."""
+    from onecomp_runtime import _hip
+
+    def use(kind: str) -> None:
+        monkeypatch.setenv("ONECOMP_HIP_GEMV_STREAM", "1" if kind == "stream" else "0")
+        monkeypatch.setenv("ONECOMP_HIP_GEMV_SPLIT", "1" if kind == "split" else "0")
+        _hip.gemm_workspace_bytes.cache_clear()  # workspace sizes follow the kernel
+
+    yield use
+    _hip.gemm_workspace_bytes.cache_clear()
+
+
 def _gemm_raw(mod, x, regime):
     from onecomp_runtime import kernels
 
@@ -351,12 +367,14 @@ def test_graph_capture_replays_match_eager(M):
             del other
 
 
+@pytest.mark.parametrize("kernel", ["stream", "tile"])
 @pytest.mark.parametrize("kind", ["gs32_v1", "v2", "actorder", "gs26", "gs128", "fp16", "bf16_scales"])
 @pytest.mark.parametrize("M", [1, 2])
-def test_decode_kernel_one_hot_bit_exact(kind, M):
-    """The decode (dot2, factored-scale) kernel reproduces dequantized rows exactly."""
+def test_decode_kernel_one_hot_bit_exact(kind, M, kernel, decode_kernel):
+    """The decode (dot2, factored-scale) kernels reproduce dequantized rows exactly."""
     from onecomp_runtime import synthetic
 
+    decode_kernel(kernel)
     K, N = 1024, 320
     kw = dict(seed=71)
     dtype = torch.float16 if kind == "fp16" else torch.bfloat16
@@ -379,21 +397,23 @@ def test_decode_kernel_one_hot_bit_exact(kind, M):
         ks = rng.choice(K, M, replace=False)
         x = torch.zeros((M, K), dtype=dtype)
         x[torch.arange(M), torch.from_numpy(ks)] = 1.0
-        say(f"decode one-hot kind={kind} M={M} rep={rep}")
+        say(f"decode one-hot {kernel} kind={kind} M={M} rep={rep}")
         out = _gemm_raw(mod, x.to(DEV), DOT)
         assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
 
 
+@pytest.mark.parametrize("kernel", ["stream", "tile"])
 @pytest.mark.parametrize("K,N", [(32, 8), (1000, 200), (5120, 1024), (4096, 4096), (2048, 17408)])
 @pytest.mark.parametrize("M", [1, 2])
 @pytest.mark.parametrize("act", [False, True])
-def test_decode_kernel_matches_oracle(K, N, M, act):
+def test_decode_kernel_matches_oracle(K, N, M, act, kernel, decode_kernel):
     from onecomp_runtime import synthetic
 
+    decode_kernel(kernel)
     layer = synthetic.gptq_layer(K, N, seed=72 + K, act_order=act)
     x = synthetic.activations(M, K, seed=73)
     mod = _module_for(layer)
-    say(f"decode kernel K={K} N={N} M={M} act={act}")
+    say(f"decode kernel {kernel} K={K} N={N} M={M} act={act}")
     assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"dot {K}x{N} M={M}")
     assert_gemm_close(mod(x.to(DEV)), _oracle_out(layer, x), "auto")
 
@@ -401,28 +421,32 @@ def test_decode_kernel_matches_oracle(K, N, M, act):
 @pytest.mark.parametrize("K,N,gs,act", [(52, 16, 26, False), (1004, 200, 32, True), (1004, 72, 32, False),
                                          (12, 8, 32, False), (4100, 64, 128, True)])
 @pytest.mark.parametrize("M", [1, 2])
-def test_decode_kernel_ragged_k(K, N, gs, act, M):
+@pytest.mark.parametrize("kernel", ["stream", "tile"])
+def test_decode_kernel_ragged_k(K, N, gs, act, M, kernel, decode_kernel):
     """K % 8 != 0 and padded groups: the decode staging scatters the tail rows
     one by one and leaves padding rows zero."""
     from onecomp_runtime import synthetic
 
+    decode_kernel(kernel)
     layer = synthetic.gptq_layer(K, N, seed=76 + K, groupsize=gs, act_order=act)
     x = synthetic.activations(M, K, seed=77)
     mod = _module_for(layer)
     assert mod.kmap is not None and mod.kinv is not None
-    say(f"decode ragged K={K} N={N} gs={gs} act={act} M={M}")
+    say(f"decode ragged {kernel} K={K} N={N} gs={gs} act={act} M={M}")
     assert_gemm_close(_gemm_raw(mod, x.to(DEV), DOT), _oracle_out(layer, x), f"ragged dot K={K}")
 
 
-def test_decode_regime_gathers_through_kmap():
+@pytest.mark.parametrize("kernel", ["stream", "tile"])
+def test_decode_regime_gathers_through_kmap(kernel, decode_kernel):
     """The decode kernel gathers act-order activations through kmap itself:
     kinv is optional, and with or without it the result is the same."""
     from onecomp_runtime import kernels, synthetic
 
+    decode_kernel(kernel)
     layer = synthetic.gptq_layer(1024, 64, seed=78, act_order=True)
     mod = _module_for(layer)
     x = synthetic.activations(1, 1024, seed=79).to(DEV)
-    say("decode without kinv")
+    say(f"decode without kinv ({kernel})")
     out = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, regime=DOT)
     assert_gemm_close(out, _oracle_out(layer, x.cpu()), "decode without kinv")
     with_kinv = kernels.int4_gemm(x, mod.tiled(), in_features=1024, kmap=mod.kmap, kinv=mod.kinv, regime=DOT)
@@ -434,6 +458,11 @@ def test_decode_regime_gathers_through_kmap():
 # -- split-item decode kernel (act-order without kinv; K beyond the LDS of the
 # whole-tile kernel): K split over workgroups, partials summed in split order by
 # the last workgroup of each tile group (device-scope counters that reset). ---
+@pytest.fixture
+def split_kernel(decode_kernel):
+    decode_kernel("split")
+
+
 def _split_gemv(mod, x, bias=None):
     from onecomp_runtime import kernels
 
@@ -442,7 +471,7 @@ def _split_gemv(mod, x, bias=None):
 
 @pytest.mark.parametrize("K,N", [(5120, 5120), (17408, 5120), (5120, 1024), (1040, 200), (2048, 17408)])
 @pytest.mark.parametrize("M", [1, 2])
-def test_split_gemv_matches_oracle(K, N, M):
+def test_split_gemv_matches_oracle(K, N, M, split_kernel):
     from onecomp_runtime import synthetic
 
     kw = dict(seed=90 + K + M, act_order=True)
@@ -456,7 +485,7 @@ def test_split_gemv_matches_oracle(K, N, M):
 
 
 @pytest.mark.parametrize("M", [1, 2])
-def test_split_gemv_one_hot_bit_exact(M):
+def test_split_gemv_one_hot_bit_exact(M, split_kernel):
     from onecomp_runtime import synthetic
 
     K, N = 4096, 320
@@ -473,7 +502,7 @@ def test_split_gemv_one_hot_bit_exact(M):
         assert np.array_equal(bits16(_split_gemv(mod, x.to(DEV))), oracle_bits(wd[:, ks].T, torch.bfloat16))
 
 
-def test_split_gemv_bias_fp16_deterministic_and_graph():
+def test_split_gemv_bias_fp16_deterministic_and_graph(split_kernel):
     from onecomp_runtime import synthetic
 
     K, N = 8192, 1024
@@ -498,18 +527,110 @@ def test_split_gemv_bias_fp16_deterministic_and_graph():
         assert torch.equal(_split_gemv(mod16, xd, bd), out)
 
 
-def test_split_gemv_beyond_whole_tile_lds():
-    """K = 65536 does not fit the whole-tile kernel's activation staging: the
-    split kernel takes it, also without act-order."""
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_beyond_whole_tile_lds(M):
+    """K = 65536 fits neither the whole-tile kernel's activation staging nor,
+    for M = 2, the stream kernel's: the automatic choice still serves it
+    (stream kernel for M = 1, split kernel for M = 2)."""
     from onecomp_runtime import synthetic
 
     K, N = 65536, 96
     layer = synthetic.gptq_layer(K, N, seed=97)
     mod = _module_for(layer)
-    x = synthetic.activations(1, K, seed=98)
-    say("split gemv K=65536")
+    x = synthetic.activations(M, K, seed=98)
+    say(f"decode K=65536 M={M}")
     out = mod(x.to(DEV))
-    assert_gemm_close(out, _oracle_out(layer, x), "split gemv K=65536")
+    assert_gemm_close(out, _oracle_out(layer, x), f"decode K=65536 M={M}")
+
+
+# -- stream decode kernel (layers with 256..1536 tiles of 16 columns): each
+# workgroup streams an equal range of (tile, 4 K steps) units; a tile cut by a
+# range boundary is finished by the second of its two workgroups, which swaps
+# in its fp32 partial and gets the first's back (64-bit cells that reset). ---
+@pytest.mark.parametrize("K,N,kind", [
+    (96, 4096, "plain"),      # 3 K steps (unit = whole tile, lanes past the end): one tile per workgroup
+    (160, 4104, "actorder"),  # 5 K steps, 257 tiles with a half tile: cut tiles
+    (64, 24576, "plain"),     # 1536 tiles of one unit: 6 tiles per workgroup
+    (128, 20000, "kmap"),     # act-order gathered through kmap (no kinv), ragged last tile
+    (17408, 5120, "actorder"),
+    (5120, 17408, "kmap"),
+    (4096, 5120, "plain"),
+    (1040, 4104, "gs26"),     # padded groups: zero rows in the staged activations
+])
+@pytest.mark.parametrize("M", [1, 2])
+def test_stream_gemv_range_cuts(K, N, kind, M, decode_kernel):
+    from onecomp_runtime import kernels, synthetic
+
+    decode_kernel("stream")
+    kw = dict(seed=120 + K % 97 + N % 89)
+    if kind in ("actorder", "kmap"):
+        kw["act_order"] = True
+    if kind == "gs26":
+        kw["groupsize"] = 26
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer)
+    x = synthetic.activations(M, K, seed=121)
+    say(f"stream gemv K={K} N={N} kind={kind} M={M}")
+    kinv = None if kind == "kmap" else mod.kinv
+    out = kernels.int4_gemm(x.to(DEV), mod.tiled(), in_features=K, kmap=mod.kmap, kinv=kinv, regime=DOT)
+    assert_gemm_close(out, _oracle_out(layer, x), f"stream gemv K={K} N={N} {kind} M={M}")
+
+
+def test_stream_gemv_deterministic_and_graph(decode_kernel):
+    """Cut tiles finished through the swap cells: repeated calls and graph
+    replays (which reuse the cells) give identical bits."""
+    from onecomp_runtime import synthetic
+
+    decode_kernel("stream")
+    K, N = 5120, 4104
+    layer = synthetic.gptq_layer(K, N, seed=122, act_order=True)
+    mod16 = _module_for(layer, torch.float16)
+    x = synthetic.activations(2, K, seed=123, dtype=torch.float16)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(124)).to(torch.float16)
+    xd, bd = x.to(DEV), bias.to(DEV)
+    say("stream gemv fp16 + bias, repeated")
+    out = _gemm_bias(mod16, xd, bd)
+    assert_gemm_close(out, _oracle_out(layer, x, "f16", bias), "stream gemv fp16 bias")
+    for rep in range(5):
+        assert torch.equal(_gemm_bias(mod16, xd, bd), out), f"rep {rep} differs"
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = _gemm_bias(mod16, xd, bd)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, out), f"graph replay {rep} differs"
+        assert torch.equal(_gemm_bias(mod16, xd, bd), out)
+
+
+def _gemm_bias(mod, x, bias):
+    from onecomp_runtime import kernels
+
+    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, kinv=mod.kinv, bias=bias,
+                             regime=DOT)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+def test_decode_kernels_agree(M, decode_kernel):
+    """The three decode kernels compute the same products (fp32 sums in
+    different orders): each within the tolerance of the oracle and close to
+    one another."""
+    from onecomp_runtime import synthetic
+
+    K, N = 5120, 5120
+    layer = synthetic.gptq_layer(K, N, seed=125, act_order=True)
+    mod = _module_for(layer)
+    x = synthetic.activations(M, K, seed=126).to(DEV)
+    ref = _oracle_out(layer, x.cpu())
+    outs = {}
+    for kernel in ("stream", "tile", "split"):
+        decode_kernel(kernel)
+        say(f"decode kernels agree: {kernel} M={M}")
+        outs[kernel] = _gemm_raw(mod, x, DOT)
+        assert_gemm_close(outs[kernel], ref, kernel)
+    for kernel in ("tile", "split"):
+        diff = (outs[kernel].float() - outs["stream"].float()).abs().max().item()
+        assert diff <= 2e-2 * outs["stream"].float().abs().max().item(), (kernel, diff)
 
 
 @pytest.mark.parametrize("regime", [DOT, SPLITK, TILED])
