@@ -76,22 +76,9 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   uint4 *xpairs = sx_lds;                                            // [MR][KS4 * 4]
   float2 *xsum = reinterpret_cast<float2 *>(sx_lds + MR * KS4 * 4);  // [MR][KS4]: (sum, B * sum)
   float *red = reinterpret_cast<float *>(xsum + MR * KS4);           // [SNTL][SW][MR][16]
-
-  // Zeros: the parked tile sums, and the padding steps [KS, KS4) of every
-  // row (a unit's lanes past the last K step multiply zeros).
-  for (int i = tid; i < SNTL * SW * MR * 16; i += SNT) red[i] = 0.f;
-  const int pad = 4 * (KS4 - KS);
-  for (int i = tid; i < MR * pad; i += SNT) {
-    const int m = i / pad, j = i - m * pad;
-    xpairs[(m * KS4 + KS) * 4 + j] = make_uint4(0, 0, 0, 0);
-    if (j < KS4 - KS) xsum[m * KS4 + KS + j] = make_float2(0.f, 0.f);
-  }
-  if constexpr (SX == SX_SCATTER) {
-    if (p.K_logical != p.K_phys) {  // physical rows without a source stay zero
-      for (int i = tid; i < MR * KS4 * 4; i += SNT) xpairs[i] = make_uint4(0, 0, 0, 0);
-      barrier_no_fence();
-    }
-  }
+  // 16-bit slot that takes the scatter's writes for rows without a place.
+  const int trash16 = static_cast<int>(reinterpret_cast<uint16_t *>(red + SNTL * SW * MR * 16) -
+                                       reinterpret_cast<uint16_t *>(xpairs));
 
   // ---- activation staging, batch by batch; the weight stream starts after
   // the first batch's loads so both are in flight together ----
@@ -132,19 +119,21 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     for (int u = 0; u < SB; ++u) {
       const int i = base + SNT * u + tid;
       if constexpr (SX == SX_SCATTER) {
-        if (i < n_items) {
-          uint16_t *x16 = reinterpret_cast<uint16_t *>(xpairs);
-          const int K_phys = p.K_phys;
-          const uint32_t rw[4] = {rr[u].x, rr[u].y, rr[u].z, rr[u].w};
+        // Branch-free within a wave: an octet past the end or a row without
+        // a physical place writes the trash slot; waves wholly past the end
+        // skip the slot.
+        if (base + SNT * u + (tid & ~63) >= n_items) continue;
+        uint16_t *x16 = reinterpret_cast<uint16_t *>(xpairs);
+        const int K_phys = i < n_items ? p.K_phys : 0;
+        const uint32_t rw[4] = {rr[u].x, rr[u].y, rr[u].z, rr[u].w};
 #pragma unroll
-          for (int m = 0; m < MR; ++m) {
-            const uint32_t xw[4] = {xr[m][u].x, xr[m][u].y, xr[m][u].z, xr[m][u].w};
+        for (int m = 0; m < MR; ++m) {
+          const uint32_t xw[4] = {xr[m][u].x, xr[m][u].y, xr[m][u].z, xr[m][u].w};
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r0 = static_cast<int>(rw[j] & 0xFFFFu), r1 = static_cast<int>(rw[j] >> 16);
-              if (r0 < K_phys) x16[xpair_slot(m, 32 * KS4, r0)] = static_cast<uint16_t>(xw[j]);
-              if (r1 < K_phys) x16[xpair_slot(m, 32 * KS4, r1)] = static_cast<uint16_t>(xw[j] >> 16);
-            }
+          for (int j = 0; j < 4; ++j) {
+            const int r0 = static_cast<int>(rw[j] & 0xFFFFu), r1 = static_cast<int>(rw[j] >> 16);
+            x16[r0 < K_phys ? xpair_slot(m, 32 * KS4, r0) : trash16] = static_cast<uint16_t>(xw[j]);
+            x16[r1 < K_phys ? xpair_slot(m, 32 * KS4, r1) : trash16] = static_cast<uint16_t>(xw[j] >> 16);
           }
         }
       } else {
@@ -180,14 +169,30 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   // the weight prefetch follows, so both are in flight together. Longer or
   // ragged rows are staged before the weight stream starts.
   const bool one_batch = n_items <= SNT * SB && (SX != SX_SCATTER || (p.K_logical & 7) == 0);
+  if (one_batch && n_items > 0) stage_load(0);
+
+  // Zeros (while the activations load): the parked tile sums, and the
+  // padding steps [KS, KS4) of every row (a unit's lanes past the last K
+  // step multiply zeros).
+  for (int i = tid; i < SNTL * SW * MR * 16; i += SNT) red[i] = 0.f;
+  const int pad = 4 * (KS4 - KS);
+  for (int i = tid; i < MR * pad; i += SNT) {
+    const int m = i / pad, j = i - m * pad;
+    xpairs[(m * KS4 + KS) * 4 + j] = make_uint4(0, 0, 0, 0);
+    if (j < KS4 - KS) xsum[m * KS4 + KS + j] = make_float2(0.f, 0.f);
+  }
+  if constexpr (SX == SX_SCATTER) {
+    if (p.K_logical != p.K_phys) {  // physical rows without a source stay zero
+      for (int i = tid; i < MR * KS4 * 4; i += SNT) xpairs[i] = make_uint4(0, 0, 0, 0);
+      barrier_no_fence();
+    }
+  }
   if (!one_batch) {
     for (int base = 0; base < n_items; base += SNT * SB) {
       stage_load(base);
       stage_store(base);
     }
     scatter_tail();
-  } else if (n_items > 0) {
-    stage_load(0);
   }
 
   // ---- weight stream: producer position (wave-uniform) and its prefetch ----
@@ -357,7 +362,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
 size_t gemv_stream_lds_bytes(int MR, int KS) {
   const size_t KS4 = static_cast<size_t>(KS + 3) / 4 * 4;
   return static_cast<size_t>(MR) * KS4 * (4 * sizeof(uint4) + sizeof(float2)) +
-         static_cast<size_t>(SNTL) * SW * MR * 16 * sizeof(float);
+         static_cast<size_t>(SNTL) * SW * MR * 16 * sizeof(float) + 16;  // + the scatter's trash slot
 }
 
 int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
@@ -392,7 +397,7 @@ static void launch_stream_t(const GemmParams &p, int nwg, hipStream_t s) {
 
 template <int DT, int SDT, int MR, int SX>
 static void launch_stream_pf(const GemmParams &p, int nwg, hipStream_t s) {
-  constexpr int PF = 3;  // units in flight per wave (measured: 3 beats 4, 6 and 8)
+  constexpr int PF = 2;  // units in flight per wave (measured: 2 beats 1, 3, 4, 6 and 8, and a deeper head start through LDS)
   if (p.KS % 4 == 0) launch_stream_t<DT, SDT, MR, SX, PF, true>(p, nwg, s);
   else launch_stream_t<DT, SDT, MR, SX, PF, false>(p, nwg, s);
 }
