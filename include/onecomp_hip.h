@@ -173,7 +173,8 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  *   bias     NULL or [N] of bias_dtype in {F16, BF16, F32}
  *   c        [M, N] (row stride ldc elements) of a_dtype
  * Constraints: N % 8 == 0, K_phys % 32 == 0, group_rows % 32 == 0,
- * K_phys % group_rows == 0; without kmap K_logical == K_phys.
+ * K_phys % group_rows == 0; without kmap K_logical == K_phys; the layer's
+ * packed words below 2 GiB (N * K_phys / 2 bytes, 16 columns per tile).
  * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned) starts
  * with a 128 KB counter area (decode calls: arrival counters and the 64-bit
  * cells through which two workgroups sharing an output tile exchange their

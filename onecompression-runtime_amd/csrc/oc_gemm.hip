@@ -1277,8 +1277,8 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   if (!aligned(qt, 16) || !aligned(kmap, 16) || !aligned(kinv, 16))
     return fail(OC_ERR_SHAPE, "qweight, kmap and kinv must be 16-byte aligned");
   const int64_t tiles = (N + TILE_N - 1) / TILE_N;
-  if (tiles * (K_phys / 32) * 64 >= (1LL << 31))
-    return fail(OC_ERR_UNSUPPORTED, "layer too large for 32-bit tile offsets");
+  if (tiles * (K_phys / 32) * 256 >= (1LL << 31))  // kernels address the words with 32-bit byte offsets
+    return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more");
   if (regime == OC_REGIME_SPLITK && M > 64)
     return fail(OC_ERR_UNSUPPORTED, "small-M regime supports M <= 64, got M=%d", M);
   if (regime == OC_REGIME_DOT && !dot_eligible(M, K_phys, group_rows))

@@ -68,7 +68,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   const int KS = p.KS, QT = (KS + 3) >> 2, KS4 = 4 * QT;  // LDS rows padded to whole units
   const int M = p.M;
   const int tiles = (p.N + TILE_N - 1) / TILE_N;
-  const int U = tiles * QT;  // < 2^23 (host: tile offsets fit 31 bits)
+  const int U = tiles * QT;  // < 2^21 (host: packed words below 2 GiB)
   const int nwg = gridDim.x, b = blockIdx.x;
   const int rq = U / nwg, rm = U % nwg;
   const int u0 = range_start(b, rq, rm), u1 = range_start(b + 1, rq, rm);

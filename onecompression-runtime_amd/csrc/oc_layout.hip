@@ -193,8 +193,8 @@ int oc_int4_prepare(const int32_t *qweight, int32_t K, int32_t N, const int32_t 
     return fail(OC_ERR_SHAPE, "bad shape K=%d N=%d K_phys=%d group_rows=%d", K, N, K_phys, group_rows);
   const int tiles = (N + TILE_N - 1) / TILE_N;
   const int KS = K_phys / 32, G = K_phys / group_rows;
-  if (static_cast<int64_t>(tiles) * KS * 64 >= (1LL << 31))
-    return fail(OC_ERR_UNSUPPORTED, "layer too large for 32-bit tile offsets (K_phys=%d N=%d)", K_phys, N);
+  if (static_cast<int64_t>(tiles) * KS * 256 >= (1LL << 31))  // kernels address the words with 32-bit byte offsets
+    return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more (K_phys=%d N=%d)", K_phys, N);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t words = static_cast<int64_t>(tiles) * KS * 64;
   hipLaunchKernelGGL(prepare_words_kernel, dim3(grid_of(words)), dim3(256), 0, s, qweight, K, N, kmap, KS, tiles,
