@@ -416,174 +416,169 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
 
 // ---------------------------------------------------------------------------
 // LDS-tiled kernel. BM = 16*WM rows, BN = 64*WN columns (4 waves x WN tiles).
-// grid = (ceil(N/BN), ceil(M/BM), ksplit) or, grouped, (ceil(N/BN), 1, E).
+// grid = (ceil(N/BN), ceil(M/BM), ksplit).
 constexpr int A_LDS_STRIDE = 40;  // halves per LDS row: 32 data + 8 pad (80 B)
 
-template <int DT, int SDT, int WM, int WN, int FMT, bool MOE>
+// RDT (RTN): the dtype of both scales and zeros when they share a 16-bit one
+// (raw loads, converted at use), else 0 (any dtypes, converted as loaded).
+template <int DT, int SDT, int WM, int WN, int FMT, int RDT>
 __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
+  // PF K steps in flight in registers (activation chunks, weight words and
+  // group parameters of each step); the activation tile of the next step is
+  // written to the other LDS buffer once its loads are in, and the step ends
+  // with an LDS-only barrier, so the loads of later steps stay in flight.
+  // Loads of steps past the range and of rows / columns past the matrix read
+  // clamped (valid) addresses; their results are never used or stored.
   constexpr int BM = 16 * WM;
   constexpr int BN = 64 * WN;
+  constexpr int PF = 2;  // measured on RTN M=512: 2 beats 4 and 8
   __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * A_LDS_STRIDE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int n0 = blockIdx.x * BN;
   const int tw = n0 / TILE_N + wave * WN;  // first tile of this wave
+  const int last_tile = (p.N - 1) / TILE_N;
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
+  const int m0 = blockIdx.y * BM;
+  const int ks_begin = blockIdx.z * p.ksteps_per_split;
+  const int ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
+  const int nsteps = max(ks_end - ks_begin, 0);
 
-  const void *qw = p.qw;
-  const void *scales = p.scales;
-  const void *zeros = p.zeros;
-  int row_end = p.M, m_first;
-  if constexpr (MOE) {
-    const int e = blockIdx.z;
-    m_first = p.expert_offsets[e];
-    row_end = p.expert_offsets[e + 1];
-    qw = static_cast<const uint32_t *>(p.qw) + e * p.qw_expert_stride;
-    scales = static_cast<const uint16_t *>(p.scales) + e * p.s_expert_stride;
-    zeros = static_cast<const uint32_t *>(p.zeros) + e * p.z_expert_stride;
-  } else {
-    m_first = blockIdx.y * BM;
+  constexpr int A_CHUNKS = BM * 4;  // 16-byte chunks of an activation tile (a multiple of 256)
+  constexpr int A_PER_THREAD = A_CHUNKS / 256;
+  const uint16_t *src_row[A_PER_THREAD];
+#pragma unroll
+  for (int i = 0; i < A_PER_THREAD; ++i) {
+    const int ch = tid + 256 * i;
+    src_row[i] = a + static_cast<int64_t>(min(m0 + (ch >> 2), p.M - 1)) * p.lda + 8 * (ch & 3);
   }
-  int ks_begin = 0, ks_end = p.KS;
-  if constexpr (!MOE) {
-    ks_begin = blockIdx.z * p.ksteps_per_split;
-    ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
-  }
-
-  constexpr int A_CHUNKS = BM * 4;
-  constexpr int A_PER_THREAD = (A_CHUNKS + 255) / 256;
-
-  for (int m0 = m_first; m0 < (MOE ? row_end : m_first + 1); m0 += BM) {
-    const uint16_t *src_row[A_PER_THREAD];
+  // Stage registers: per step in flight, the activation chunks, weight
+  // words and group parameters (GPTQ: scale bits and zero word; RTN: scale
+  // and zero as RDT bits, or as fp32 bits). Separate arrays indexed by
+  // compile-time stage numbers stay in registers.
+  uint32_t sa[PF][A_PER_THREAD * 4];
+  uint32_t sq[PF][WN], ss[PF][WN], sz[PF][WN];
+  auto load = [&](auto fc, int ks) __attribute__((always_inline)) {
+    constexpr int f = decltype(fc)::value;
+    ks = min(ks, max(ks_end - 1, 0));
+#pragma unroll
+    for (int i = 0; i < A_PER_THREAD; ++i) {
+      const uint4 v = *reinterpret_cast<const uint4 *>(src_row[i] + 32 * ks);
+      sa[f][4 * i] = v.x;
+      sa[f][4 * i + 1] = v.y;
+      sa[f][4 * i + 2] = v.z;
+      sa[f][4 * i + 3] = v.w;
+    }
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int tl = min(tw + j, last_tile);
+      sq[f][j] = load_word<FMT>(p, p.qw, tl, ks, quad, c16);
+      if constexpr (FMT == FMT_GPTQ) {
+        const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
+        ss[f][j] = static_cast<const uint16_t *>(p.scales)[tgs * TILE_N + c16];
+        sz[f][j] = static_cast<const uint32_t *>(p.zeros)[tgs * 2 + (c16 >> 3)];
+      } else {
+        const int n = min(TILE_N * tl + c16, p.N - 1);
+        const int64_t i = static_cast<int64_t>(n) * p.rtn_G + (32 * ks + 8 * quad) / p.rtn_gs;
+        if constexpr (RDT != 0) {
+          ss[f][j] = static_cast<const uint16_t *>(p.scales)[i];
+          sz[f][j] = static_cast<const uint16_t *>(p.zeros)[i];
+        } else {
+          ss[f][j] = __float_as_uint(load_any_f32(p.scales, i, p.scale_dtype));
+          sz[f][j] = __float_as_uint(load_any_f32(p.zeros, i, p.zero_dtype));
+        }
+      }
+    }
+  };
+  auto store_a = [&](int buf, auto fc) __attribute__((always_inline)) {
+    constexpr int f = decltype(fc)::value;
 #pragma unroll
     for (int i = 0; i < A_PER_THREAD; ++i) {
       const int ch = tid + 256 * i;
-      const int r = m0 + (ch >> 2);
-      src_row[i] = nullptr;
-      if (ch < A_CHUNKS && r < row_end) {
-        int64_t arow = r;
-        if constexpr (MOE) arow = p.sorted_pairs[r] / p.topk;
-        src_row[i] = a + arow * p.lda;
-      }
+      *reinterpret_cast<uint4 *>(&As[buf][(ch >> 2) * A_LDS_STRIDE + 8 * (ch & 3)]) =
+          make_uint4(sa[f][4 * i], sa[f][4 * i + 1], sa[f][4 * i + 2], sa[f][4 * i + 3]);
     }
-    auto load_a_tile = [&](int ks, uint4 (&areg)[A_PER_THREAD]) {
+  };
+
+  // The prologue issues each step's loads in the loop's order.
+  static_for<0, PF>([&](auto fc) __attribute__((always_inline)) {
+    load(fc, ks_begin + decltype(fc)::value);
+    __builtin_amdgcn_sched_barrier(0);
+  });
+  v4f32 acc[WM][WN];
 #pragma unroll
-      for (int i = 0; i < A_PER_THREAD; ++i) {
-        const int ch = tid + 256 * i;
-        areg[i] = src_row[i] ? *reinterpret_cast<const uint4 *>(src_row[i] + 32 * ks + 8 * (ch & 3))
-                             : make_uint4(0, 0, 0, 0);
-      }
-    };
-    auto store_a_tile = [&](int buf, const uint4 (&areg)[A_PER_THREAD]) {
+  for (int t = 0; t < WM; ++t)
 #pragma unroll
-      for (int i = 0; i < A_PER_THREAD; ++i) {
-        const int ch = tid + 256 * i;
-        if (ch < A_CHUNKS)
-          *reinterpret_cast<uint4 *>(&As[buf][(ch >> 2) * A_LDS_STRIDE + 8 * (ch & 3)]) = areg[i];
-      }
-    };
-    uint32_t qreg[WN];
-    auto load_w = [&](int ks) {
+    for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+  if (nsteps > 0) store_a(0, ic<0>{});
+  barrier_no_fence();
+
+  const int nsteps_pad = (nsteps + PF - 1) / PF * PF;
+  for (int i0 = 0; i0 < nsteps_pad; i0 += PF) {
+    static_for<0, PF>([&](auto fc) __attribute__((always_inline)) {
+      constexpr int f = decltype(fc)::value;
+      const int i = i0 + f;  // step ks_begin + i sits in stage f; refilled once consumed
+      if (i < nsteps) {      // uniform over the workgroup
+        uint4 b[WN];
 #pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const int n = TILE_N * (tw + j) + c16;
-        qreg[j] = n < p.N ? load_word<FMT>(p, qw, tw + j, ks, quad, c16) : 0u;
-      }
-    };
-    auto dequant_w = [&](int ks, uint4 (&b)[WN]) {
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        if constexpr (FMT == FMT_GPTQ) {
-          const int g = group_of(p, ks);
-          const int tl = min(tw + j, (p.N - 1) / TILE_N);  // keep metadata reads inside the tensor
-          const int64_t tgs = static_cast<int64_t>(tl) * p.G + g;
-          const uint16_t sb = static_cast<const uint16_t *>(scales)[tgs * TILE_N + c16];
-          const uint32_t zw = static_cast<const uint32_t *>(zeros)[tgs * 2 + (c16 >> 3)];
-          b[j] = dequant8<DT>(qreg[j], make_group_param(scale_f32<SDT>(sb), tile_zero(zw, c16)));
-        } else {
-          const int n = min(TILE_N * (tw + j) + c16, p.N - 1);
-          b[j] = rtn_dequant8<DT>(qreg[j], rtn_param<DT>(p, (32 * ks + 8 * quad) / p.rtn_gs, n));
+        for (int j = 0; j < WN; ++j) {
+          if constexpr (FMT == FMT_GPTQ) {
+            b[j] = dequant8<DT>(sq[f][j], make_group_param(scale_f32<SDT>(ss[f][j]), tile_zero(sz[f][j], c16)));
+          } else {
+            RtnParam rp;
+            if constexpr (RDT != 0) {
+              rp.sq = round_to<DT>(half_to_f32<RDT>(ss[f][j]));
+              rp.zq = round_to<DT>(half_to_f32<RDT>(sz[f][j]));
+            } else {
+              rp.sq = round_to<DT>(__uint_as_float(ss[f][j]));
+              rp.zq = round_to<DT>(__uint_as_float(sz[f][j]));
+            }
+            b[j] = rtn_dequant8<DT>(sq[f][j], rp);
+          }
         }
+#pragma unroll
+        for (int t = 0; t < WM; ++t) {
+          const uint4 av = *reinterpret_cast<const uint4 *>(&As[i & 1][(16 * t + c16) * A_LDS_STRIDE + 8 * quad]);
+#pragma unroll
+          for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
+        }
+        if (i + 1 < nsteps) store_a((i + 1) & 1, ic<(f + 1) % PF>{});
       }
-    };
+      load(fc, ks_begin + i + PF);
+      barrier_no_fence();  // the next step's activations are in LDS; this step's reads are done
+    });
+  }
 
-    v4f32 acc[WM][WN];
+  // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
+  if (p.ksplit == 1) {
 #pragma unroll
-    for (int t = 0; t < WM; ++t)
-#pragma unroll
-      for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
-
-    uint4 areg[A_PER_THREAD];
-    if (ks_begin < ks_end) {
-      load_a_tile(ks_begin, areg);
-      load_w(ks_begin);
-      store_a_tile(0, areg);
-    }
-    __syncthreads();
-    for (int ks = ks_begin; ks < ks_end; ++ks) {
-      const int buf = (ks - ks_begin) & 1;
-      uint4 b[WN];
-      dequant_w(ks, b);
-      const bool has_next = ks + 1 < ks_end;
-      if (has_next) {
-        load_a_tile(ks + 1, areg);
-        load_w(ks + 1);
-      }
-#pragma unroll
-      for (int t = 0; t < WM; ++t) {
-        const uint4 av = *reinterpret_cast<const uint4 *>(&As[buf][(16 * t + c16) * A_LDS_STRIDE + 8 * quad]);
-#pragma unroll
-        for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
-      }
-      if (has_next) store_a_tile(buf ^ 1, areg);
-      __syncthreads();
-    }
-
-    // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
-    if constexpr (MOE) {
+    for (int j = 0; j < WN; ++j) {
+      const int n = TILE_N * (tw + j) + c16;
+      if (n >= p.N) continue;
+      const float bv = bias_at(p, n);
 #pragma unroll
       for (int t = 0; t < WM; ++t)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m0 + 16 * t + 4 * quad + i;
-          if (r >= row_end) continue;
-          const int64_t orow = p.sorted_pairs[r];
-#pragma unroll
-          for (int j = 0; j < WN; ++j) {
-            const int n = TILE_N * (tw + j) + c16;
-            if (n < p.N) store_c<DT>(p.c, orow * p.ldc + n, acc[t][j][i]);
-          }
+          if (r < p.M) store_c<DT>(p.c, static_cast<int64_t>(r) * p.ldc + n, acc[t][j][i] + bv);
         }
-    } else if (p.ksplit == 1) {
+    }
+  } else {
+    // split-K: fp32 partials; splitk_reduce_kernel sums them in split order
+    float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
 #pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const int n = TILE_N * (tw + j) + c16;
-        if (n >= p.N) continue;
-        const float bv = bias_at(p, n);
+    for (int j = 0; j < WN; ++j) {
+      const int n = TILE_N * (tw + j) + c16;
+      if (n >= p.N) continue;
 #pragma unroll
-        for (int t = 0; t < WM; ++t)
+      for (int t = 0; t < WM; ++t)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = m0 + 16 * t + 4 * quad + i;
-            if (r < p.M) store_c<DT>(p.c, static_cast<int64_t>(r) * p.ldc + n, acc[t][j][i] + bv);
-          }
-      }
-    } else {
-      // split-K: fp32 partials; splitk_reduce_kernel sums them in split order
-      float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
-#pragma unroll
-      for (int j = 0; j < WN; ++j) {
-        const int n = TILE_N * (tw + j) + c16;
-        if (n >= p.N) continue;
-#pragma unroll
-        for (int t = 0; t < WM; ++t)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = m0 + 16 * t + 4 * quad + i;
-            if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
-          }
-      }
+        for (int i = 0; i < 4; ++i) {
+          const int r = m0 + 16 * t + 4 * quad + i;
+          if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
+        }
     }
   }
 }
@@ -1182,7 +1177,15 @@ void launch_mfma(const GemmParams &p, int mt, hipStream_t s) {
 template <int DT, int SDT, int WM, int WN, int FMT>
 void launch_tiled_t(const GemmParams &p, hipStream_t s) {
   const dim3 grid((p.N + 64 * WN - 1) / (64 * WN), (p.M + 16 * WM - 1) / (16 * WM), p.ksplit);
-  hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, false>), grid, dim3(256), 0, s, p);
+  const bool same16 = FMT == FMT_RTN && p.scale_dtype == p.zero_dtype;
+  if (same16 && p.scale_dtype == OC_DTYPE_F16)
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, FMT == FMT_RTN ? OC_DTYPE_F16 : 0>), grid, dim3(256), 0,
+                       s, p);
+  else if (same16 && p.scale_dtype == OC_DTYPE_BF16)
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, FMT == FMT_RTN ? OC_DTYPE_BF16 : 0>), grid, dim3(256),
+                       0, s, p);
+  else
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
     hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,

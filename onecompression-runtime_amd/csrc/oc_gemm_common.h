@@ -111,6 +111,16 @@ __device__ __forceinline__ void barrier_no_fence() { asm volatile("s_waitcnt lgk
 template <int I>
 using ic = std::integral_constant<int, I>;
 
+// f(ic<k>) for k = K0 .. E - 1, unrolled at compile time (stage arrays stay
+// in registers even where the unroller would give up on a large body).
+template <int K0, int E, typename F>
+__device__ __forceinline__ void static_for(F &&f) {
+  if constexpr (K0 < E) {
+    f(ic<K0>{});
+    static_for<K0 + 1, E>(f);
+  }
+}
+
 // 16-byte chunk swizzle of the LDS activation rows (64 bytes each): chunk q
 // of row r sits at position q ^ big_swz(r). An MFMA operand read (rows
 // r0..r0+15, one chunk) then touches distinct banks within every group of 8
