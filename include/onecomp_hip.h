@@ -176,9 +176,10 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  * K_phys % group_rows == 0; without kmap K_logical == K_phys; the layer's
  * packed words below 2 GiB (N * K_phys / 2 bytes, 16 columns per tile).
  * The workspace (>= oc_int4_gemm_workspace_bytes, 256-byte aligned) starts
- * with a 128 KB counter area (decode calls: arrival counters and the 64-bit
- * cells through which two workgroups sharing an output tile exchange their
- * partial sums), then holds gathered activations (kmap with M > 2) and fp32
+ * with a 512 KB counter area (small-batch calls, M <= 16: arrival counters
+ * and the 64-bit cells through which two workgroups sharing an output tile
+ * exchange their partial sums), then holds gathered activations (kmap with
+ * M > 2, when the whole-tile kernel serves the batch) and fp32
  * split-K partials (large M with few output tiles, or a decode call whose K
  * is split over workgroups). The counter area must hold zeros the
  * first time a workspace is used (e.g. allocate it zero-filled) and every

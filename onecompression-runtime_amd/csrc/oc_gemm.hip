@@ -955,7 +955,7 @@ struct Plan {
 // partials]. The counter area holds the decode kernels' arrival counters and
 // swap cells; it must be zero when a workspace is first used and every call
 // leaves it zero, so no regime writes anything else there.
-constexpr size_t COUNTER_BYTES = 128 * 1024;
+constexpr size_t COUNTER_BYTES = 512 * 1024;
 constexpr int COUNTER_SLOTS = static_cast<int>(COUNTER_BYTES / sizeof(int));
 
 // Compute units of the current device (cached per device).
@@ -1013,7 +1013,8 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
   // Tuning knobs, read once per process.
   static const bool dot_disabled = env_int("ONECOMP_HIP_DISABLE_DOT", 0) != 0;
   static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
-  if (regime == OC_REGIME_AUTO) {
+  const bool automatic = regime == OC_REGIME_AUTO;
+  if (automatic) {
     if (!dot_disabled && dot_eligible(M, K_phys, group_rows)) regime = OC_REGIME_DOT;
     else regime = M <= 64 ? OC_REGIME_SPLITK : OC_REGIME_TILED;
   }
@@ -1057,6 +1058,18 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     return sp;
   }
   if (regime == OC_REGIME_SPLITK) {
+    // Chosen automatically, batches of 3..16 rows take the balanced-range
+    // kernel's MFMA form when their activation rows fit in LDS (it stages
+    // act-order rows itself: no gather pass). ONECOMP_HIP_GEMV_STREAM=0
+    // (read per call) keeps them on the whole-tile MFMA kernel below.
+    if (automatic && M >= 3 && M <= 16 && ilog2_exact(group_rows / 32) >= 0 &&
+        env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
+      sp.stream_wgs = gemv_stream_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
+      if (sp.stream_wgs > 0) {
+        sp.gather = false;
+        return sp;
+      }
+    }
     sp.mt = std::max(1, (M + 15) / 16);
     return sp;
   }
@@ -1311,7 +1324,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.G = K_phys / group_rows;
   p.group_rows = group_rows;
   p.gshift = ilog2_exact(group_rows / 32);
-  p.kinv = sp.regime == OC_REGIME_DOT && kmap ? kinv : nullptr;
+  p.kinv = (sp.regime == OC_REGIME_DOT || sp.stream_wgs > 0) && kmap ? kinv : nullptr;
   p.bias = bias;
   p.bias_dtype = bias_dtype;
   p.c = c;

@@ -53,6 +53,7 @@ struct GemmParams {
   // decode (split GEMV)
   const int32_t *kmap;  // physical -> logical row (-1: padding), NULL: identity
   int *counters;        // per tile group arrival counters (zero between calls)
+  int stream_slots;     // stream GEMV: most tiles one workgroup's range touches
 };
 
 __device__ __forceinline__ int group_of(const GemmParams &p, int ks) {
@@ -197,11 +198,12 @@ GemvPlan plan_gemv(int M, int N, int KS, bool gather, int cus);
 size_t gemv_lds_bytes(int MR, int S);
 void launch_gptq_gemv(const GemmParams &p, int a_dtype, int scale_dtype, int T, hipStream_t s);
 
-// Decode GEMV with one balanced weight range per workgroup
-// (oc_gemv_stream.hip). gemv_stream_wgs gives the launch width for a layer
-// (0: not applicable: M > 2, activation rows beyond LDS, fewer tiles than
-// workgroups, or more swap cells than cell_bytes hold). The launch needs
-// p.counters: nwg * M * 16 zeroed 64-bit cells, left zero.
+// Small-batch GEMV with one balanced weight range per workgroup
+// (oc_gemv_stream.hip; dot2 for M <= 2, MFMA for M <= 16). gemv_stream_wgs
+// gives the launch width for a layer (0: not applicable: M > 16, activation
+// rows beyond LDS, fewer tiles than workgroups, or more swap cells than
+// cell_bytes hold). The launch needs p.counters: nwg * MR * 16 zeroed 64-bit
+// cells (MR = M rounded up to 1, 2, 4, 8 or 16), left zero.
 int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
 void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s);
 

@@ -1,4 +1,4 @@
-// Decode GEMV (M <= 2) as one balanced weight stream per workgroup, for gfx950.
+// Small-batch GEMV (M <= 16) as one balanced weight stream per workgroup, for gfx950.
 //
 // A layer's packed weights are U = tiles x QT units of 1 KB: one 16-column
 // tile by four 32-row K steps (QT = ceil(KS / 4) units per tile), stored
@@ -29,13 +29,24 @@
 // out of each 32-row group,
 //   sum_k x_k s (w_k - z) = s (sum_k x_k (B + w_k) - (B + z) sum_k x_k),
 // with B + w_k the exact 16-bit number made by OR-ing the code into the
-// mantissa of B (bf16 128.0, fp16 1024.0), the first sum on
-// v_dot2_f32_{bf16,f16} against activation pairs in LDS and the second from
-// per-step activation sums staged beside them.
+// mantissa of B (bf16 128.0, fp16 1024.0) and the second sum from per-step
+// activation sums staged beside the activation pairs. The first sum:
+//  * M <= 2: v_dot2_f32_{bf16,f16} per lane against activation pairs in LDS;
+//  * 3 <= M <= 16 (MR = 4, 8 or 16 staged rows): one v_mfma_f32_16x16x32 per
+//    K step. Lane (g, c) loads octet g of each of the unit's four steps
+//    (four 4-byte loads; a wave instruction reads 256 consecutive bytes),
+//    which is the B operand layout of one MFMA per step (column c, K rows
+//    8 g .. 8 g + 7), against the A operand of lane (g, r): row r's pairs of
+//    octet g; output lane (g, c) holds rows 4 g + i. Each step's sum is
+//    scaled once per output; the zero term of all four steps is one
+//    v_mfma_f32_16x16x4_f32 (lane (g, c) holds the activation sum of row c
+//    over step g and -s (B + z) of column c at step g), accumulated apart
+//    and added when the tile is parked.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <atomic>
+#include <type_traits>
 
 #include "oc_gemm_common.h"
 
@@ -46,13 +57,26 @@ namespace {
 constexpr int SW = 16;        // waves per workgroup
 constexpr int SNT = 64 * SW;  // threads per workgroup
 constexpr int SNTL = 8;       // tiles one workgroup's range may touch
-constexpr int SB = 3;         // staged octets per thread per batch
 
 enum { SX_CONTIG = 0, SX_SCATTER = 1, SX_GATHER = 2 };
 
 // Balanced ranges: U = nwg q + r units; workgroups b < r own q + 1 units,
 // the others q (q >= QT: the host launches at most one workgroup per tile).
-__device__ __forceinline__ int range_start(int b, int q, int r) { return b * q + min(b, r); }
+__host__ __device__ __forceinline__ int range_start(int b, int q, int r) { return b * q + (b < r ? b : r); }
+
+// Rows staged per launch: M itself for the dot2 path, else the next of 4, 8, 16.
+int stream_rows(int M) { return M <= 2 ? M : M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : 0; }
+
+// Most tiles any workgroup's range touches (its LDS tile slots).
+int stream_slots(int64_t tiles, int QT, int nwg) {
+  const int U = static_cast<int>(tiles * QT), q = U / nwg, r = U % nwg;
+  int most = 0;
+  for (int b = 0; b < nwg; ++b) {
+    const int u0 = range_start(b, q, r), u1 = range_start(b + 1, q, r);
+    most = std::max(most, (u1 - 1) / QT - u0 / QT + 1);
+  }
+  return most;
+}
 
 }  // namespace
 
@@ -61,6 +85,9 @@ __device__ __forceinline__ int range_start(int b, int q, int r) { return b * q +
 template <int DT, int SDT, int MR, int SX, int PF, bool AL>
 __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
+  constexpr bool MF = MR > 2;     // MFMA inner product (rows 4 g + i of lane (g, c))
+  constexpr int SB = MF ? 1 : 3;  // staged octets per thread per batch
+  static_assert(!MF || MR == 4 || MR == 8 || MR == 16, "MFMA rows");
   extern __shared__ __attribute__((aligned(16))) uint4 sx_lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -73,12 +100,22 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   const int rq = U / nwg, rm = U % nwg;
   const int u0 = range_start(b, rq, rm), u1 = range_start(b + 1, rq, rm);
   const int t_first = u0 / QT, t_last = (u1 - 1) / QT;
-  uint4 *xpairs = sx_lds;                                            // [MR][KS4 * 4]
-  float2 *xsum = reinterpret_cast<float2 *>(sx_lds + MR * KS4 * 4);  // [MR][KS4]: (sum, B * sum)
-  float *red = reinterpret_cast<float *>(xsum + MR * KS4);           // [SNTL][SW][MR][16]
+  const int nslots = p.stream_slots;                                 // tiles a range touches, at most
+  // Row stride of the staged pairs, in 16-byte chunks: the MFMA form reads
+  // 16 rows at once and pads each row by one chunk (distinct banks).
+  const int RS = 4 * KS4 + (MF ? 1 : 0);
+  uint4 *xpairs = sx_lds;                                          // [MR][RS]
+  float2 *xsum = reinterpret_cast<float2 *>(sx_lds + MR * RS);  // dot2: [MR][KS4] (sum, B * sum)
+  float *xst = reinterpret_cast<float *>(sx_lds + MR * RS);     // MFMA: [KS4][MR] sums
+  float *red = MF ? xst + KS4 * MR : reinterpret_cast<float *>(xsum + MR * KS4);  // [nslots][SW][MR][16]
   // 16-bit slot that takes the scatter's writes for rows without a place.
-  const int trash16 = static_cast<int>(reinterpret_cast<uint16_t *>(red + SNTL * SW * MR * 16) -
+  const int trash16 = static_cast<int>(reinterpret_cast<uint16_t *>(red + nslots * SW * MR * 16) -
                                        reinterpret_cast<uint16_t *>(xpairs));
+  // Step sum of row m, K step ks.
+  auto put_sum = [&](int m, int ks, float sum) {
+    if constexpr (MF) xst[ks * MR + m] = sum;
+    else xsum[m * KS4 + ks] = make_float2(sum, dot_base<DT>() * sum);
+  };
 
   // ---- activation staging, batch by batch; the weight stream starts after
   // the first batch's loads so both are in flight together ----
@@ -132,8 +169,8 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const int r0 = static_cast<int>(rw[j] & 0xFFFFu), r1 = static_cast<int>(rw[j] >> 16);
-            x16[r0 < K_phys ? xpair_slot(m, 32 * KS4, r0) : trash16] = static_cast<uint16_t>(xw[j]);
-            x16[r1 < K_phys ? xpair_slot(m, 32 * KS4, r1) : trash16] = static_cast<uint16_t>(xw[j] >> 16);
+            x16[r0 < K_phys ? xpair_slot(m, 8 * RS, r0) : trash16] = static_cast<uint16_t>(xw[j]);
+            x16[r1 < K_phys ? xpair_slot(m, 8 * RS, r1) : trash16] = static_cast<uint16_t>(xw[j] >> 16);
           }
         }
       } else {
@@ -145,8 +182,8 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
           sum += __shfl_xor(sum, 1);
           sum += __shfl_xor(sum, 2);
           if (i < n_items) {
-            xpairs[m * KS4 * 4 + i] = pr;
-            if ((i & 3) == 0) xsum[m * KS4 + (i >> 2)] = make_float2(sum, dot_base<DT>() * sum);
+            xpairs[m * RS + i] = pr;
+            if ((i & 3) == 0) put_sum(m, i >> 2, sum);
           }
         }
       }
@@ -160,7 +197,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
         if (r < p.K_phys) {
 #pragma unroll
           for (int m = 0; m < MR; ++m)
-            x16[xpair_slot(m, 32 * KS4, r)] = a[static_cast<int64_t>(min(m, M - 1)) * p.lda + k];
+            x16[xpair_slot(m, 8 * RS, r)] = a[static_cast<int64_t>(min(m, M - 1)) * p.lda + k];
         }
       }
     }
@@ -174,16 +211,16 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   // Zeros (while the activations load): the parked tile sums, and the
   // padding steps [KS, KS4) of every row (a unit's lanes past the last K
   // step multiply zeros).
-  for (int i = tid; i < SNTL * SW * MR * 16; i += SNT) red[i] = 0.f;
+  for (int i = tid; i < nslots * SW * MR * 16; i += SNT) red[i] = 0.f;
   const int pad = 4 * (KS4 - KS);
   for (int i = tid; i < MR * pad; i += SNT) {
     const int m = i / pad, j = i - m * pad;
-    xpairs[(m * KS4 + KS) * 4 + j] = make_uint4(0, 0, 0, 0);
-    if (j < KS4 - KS) xsum[m * KS4 + KS + j] = make_float2(0.f, 0.f);
+    xpairs[m * RS + KS * 4 + j] = make_uint4(0, 0, 0, 0);
+    if (j < KS4 - KS) put_sum(m, KS + j, 0.f);
   }
   if constexpr (SX == SX_SCATTER) {
     if (p.K_logical != p.K_phys) {  // physical rows without a source stay zero
-      for (int i = tid; i < MR * KS4 * 4; i += SNT) xpairs[i] = make_uint4(0, 0, 0, 0);
+      for (int i = tid; i < MR * RS; i += SNT) xpairs[i] = make_uint4(0, 0, 0, 0);
       barrier_no_fence();
     }
   }
@@ -196,11 +233,22 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   }
 
   // ---- weight stream: producer position (wave-uniform) and its prefetch ----
-  struct Stage {
+  // dot2 form: lane (h, c) loads the four octets of K step 4 q + h of
+  // column c (16 bytes) and that step's scale and zero word. MFMA form: lane
+  // (h, c) loads octet h of each of the four steps (four 4-byte loads, each
+  // wave instruction 256 consecutive bytes), the four steps' scales of
+  // column c, and the zero word of its own step h (for the zero term).
+  struct StageDot {
     uint4 q;
     uint32_t s;
     uint32_t z;
   };
+  struct StageMf {
+    uint32_t q[4];
+    uint32_t s[4];
+    uint32_t z;
+  };
+  using Stage = std::conditional_t<MF, StageMf, StageDot>;
   // Buffer loads: a wave-uniform unit offset plus a fixed per-lane offset.
   // Lanes past a tile's last K step read the next tile (or past the end:
   // zero), which meets the zero padding of the staged activations; units
@@ -210,8 +258,9 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   const __amdgpu_buffer_rsrc_t q_rs = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
   const __amdgpu_buffer_rsrc_t s_rs = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * G * 32);
   const __amdgpu_buffer_rsrc_t z_rs = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * G * 8);
-  const uint32_t q_lane = lane * 16u;                                  // column c, K step 4 q + h
-  const uint32_t s_lane = static_cast<uint32_t>((h >> gs2) * 16 + c) * 2u;  // group of K step 4 q + h
+  const uint32_t q_lane = MF ? static_cast<uint32_t>(c * 16 + 4 * h) : lane * 16u;  // + 256 j (MFMA form)
+  const uint32_t s_lane = MF ? static_cast<uint32_t>(c) * 2u                          // + 32 (j >> gs2)
+                             : static_cast<uint32_t>((h >> gs2) * 16 + c) * 2u;      // group of K step 4 q + h
   const uint32_t z_lane = static_cast<uint32_t>((h >> gs2) * 2 + (c >> 3)) * 4u;
   constexpr uint32_t NOWHERE = 0xFFFFF000u;
   const int w_u0 = u0 + wave;  // this wave's first unit; it takes every SW-th from there
@@ -227,9 +276,18 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
       gb = static_cast<uint32_t>(tt * G + ((4 * qq) >> gshift));
     }
     const bool in = pu < u1;
-    const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, q_lane + (in ? qb : NOWHERE), 0, 0);
-    S.q = make_uint4(q[0], q[1], q[2], q[3]);
-    S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, s_lane + (in ? gb * 32u : NOWHERE), 0, 0);
+    const uint32_t qo = q_lane + (in ? qb : NOWHERE), so = s_lane + (in ? gb * 32u : NOWHERE);
+    if constexpr (MF) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        S.q[j] = __builtin_amdgcn_raw_buffer_load_b32(q_rs, qo + 256u * j, 0, 0);
+        S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 32 * (j >> gs2), 0);
+      }
+    } else {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0, 0);
+      S.q = make_uint4(q[0], q[1], q[2], q[3]);
+      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0, 0);
+    }
     S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * 8u : NOWHERE), 0, 0);
     pu += SW;
   };
@@ -252,13 +310,13 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
       float sum = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        const uint4 pr = xpairs[(m * KS4 + ks) * 4 + w];
+        const uint4 pr = xpairs[m * RS + ks * 4 + w];
         sum = dot2acc<DT>(pr.x, ones, sum);
         sum = dot2acc<DT>(pr.y, ones, sum);
         sum = dot2acc<DT>(pr.z, ones, sum);
         sum = dot2acc<DT>(pr.w, ones, sum);
       }
-      xsum[m * KS4 + ks] = make_float2(sum, dot_base<DT>() * sum);
+      put_sum(m, ks, sum);
     }
   }
   barrier_no_fence();  // LDS only: the weight loads stay in flight
@@ -268,17 +326,32 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   int cu = w_u0, ct = w_u0 / QT;  // consumer: unit and its tile
   int t_end = (ct + 1) * QT;      // first unit of the next tile
   int cur_t = ct;                 // tile being accumulated
-  float acc[MR];
+  constexpr int NACC = MF ? 4 : MR;
+  float acc[NACC];  // dot2: row m, lane's K step; MFMA: row 4 h + i, column c
 #pragma unroll
-  for (int m = 0; m < MR; ++m) acc[m] = 0.f;
+  for (int m = 0; m < NACC; ++m) acc[m] = 0.f;
+  // MFMA form: the zero term of the tile, accumulated by the matrix core
+  // alone and added to acc when the tile is parked. (Chaining it through
+  // acc, whose values the VALU writes, gave wrong sums for 16 rows.)
+  v4f32 zacc = {0.f, 0.f, 0.f, 0.f};
   auto flush = [&]() {
+    float *slot_red = red + ((cur_t - t_first) * SW + wave) * MR * 16;
+    if constexpr (MF) {
 #pragma unroll
-    for (int m = 0; m < MR; ++m) {
-      float v = acc[m];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      if (h == 0) red[(((cur_t - t_first) * SW + wave) * MR + m) * 16 + c] = v;
-      acc[m] = 0.f;
+      for (int i = 0; i < 4; ++i) {
+        if (4 * h + i < MR) slot_red[(4 * h + i) * 16 + c] = acc[i] + zacc[i];
+        acc[i] = 0.f;
+        zacc[i] = 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        float v = acc[m];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (h == 0) slot_red[m * 16 + c] = v;
+        acc[m] = 0.f;
+      }
     }
   };
   const int nu_pad = (nu + PF - 1) / PF * PF;
@@ -293,35 +366,75 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
         t_end = (ct + 1) * QT;
         cur_t = ct;
       }
-      const int ks = 4 * min(cu - ct * QT, QT - 1) + h;  // < KS4 (padded rows)
-      float d[MR][2];
+      const int qq = min(cu - ct * QT, QT - 1);  // unit within the tile; K steps 4 qq .. 4 qq + 3 < KS4
+      if constexpr (MF) {
+        // LDS operands first (their latency overlaps the decode): A =
+        // row c's pairs of octet h of each step (rows past MR read row
+        // MR - 1 and feed output rows that are never stored), and row c's
+        // activation sum over K step 4 qq + h.
+        const int arow = MR == 16 ? c : min(c, MR - 1);
+        const uint4 *xrow = xpairs + arow * RS + 16 * qq + h;
+        uint4 xa[4];
+        static_for<0, 4>([&](auto J) __attribute__((always_inline)) { xa[J] = xrow[4 * J]; });
+        const float xz = xst[(4 * qq + h) * MR + arow];
+        // Zero term of the unit's four steps on the matrix core: lane (h, c)
+        // holds A[c][h] = that sum and B[h][c] = -s (B + z) of its own step
+        // and column, so zacc[i] += sum_h X[4 g + i][h] * (-s (B + z))[h][c].
+        // Scale of the lane's own step h, selected without branches (a branch
+        // per case would wait for each load on its own path).
+        const uint32_t m1 = 0u - static_cast<uint32_t>(h == 1), m2 = 0u - static_cast<uint32_t>(h == 2),
+                       m3 = 0u - static_cast<uint32_t>(h == 3);
+        const uint32_t s_own = cur.s[0] ^ ((cur.s[0] ^ cur.s[1]) & m1) ^ ((cur.s[0] ^ cur.s[2]) & m2) ^
+                               ((cur.s[0] ^ cur.s[3]) & m3);
+        const float bz = -scale_f32<SDT>(s_own) * (dot_base<DT>() + static_cast<float>(tile_zero(cur.z, c)));
+        zacc = __builtin_amdgcn_mfma_f32_16x16x4f32(xz, bz, zacc, 0, 0, 0);
+        v4f32 av = {acc[0], acc[1], acc[2], acc[3]};
+        const uint32_t *oct = cur.q, *sj = cur.s;  // octet h of K step j, scale of K step j (column c)
+        // Units past the range load zero scales: they add exactly zero (finite
+        // activations), so no per-value select is needed.
 #pragma unroll
-      for (int m = 0; m < MR; ++m) d[m][0] = d[m][1] = 0.f;
-      const uint32_t qs[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t q = oct[j];
+          const uint4 bq = make_uint4(and_or(q, 0x000F000Fu, MAGIC), and_or(q >> 4, 0x000F000Fu, MAGIC),
+                                      and_or(q >> 8, 0x000F000Fu, MAGIC), and_or(q >> 12, 0x000F000Fu, MAGIC));
+          const v4f32 d = mfma16x16x32<DT>(xa[j], bq, v4f32{0.f, 0.f, 0.f, 0.f});
+          const float s = scale_f32<SDT>(sj[j]);
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t q = qs[w];
-        const uint32_t b0 = and_or(q, 0x000F000Fu, MAGIC);
-        const uint32_t b1 = and_or(q >> 4, 0x000F000Fu, MAGIC);
-        const uint32_t b2 = and_or(q >> 8, 0x000F000Fu, MAGIC);
-        const uint32_t b3 = and_or(q >> 12, 0x000F000Fu, MAGIC);
+          for (int i = 0; i < 4; ++i) av[i] = __builtin_fmaf(s, d[i], av[i]);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = av[i];
+      } else {
+        const int ks = 4 * qq + h;
+        float d[MR][2];
+#pragma unroll
+        for (int m = 0; m < MR; ++m) d[m][0] = d[m][1] = 0.f;
+        const uint32_t qs[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t q = qs[w];
+          const uint32_t b0 = and_or(q, 0x000F000Fu, MAGIC);
+          const uint32_t b1 = and_or(q >> 4, 0x000F000Fu, MAGIC);
+          const uint32_t b2 = and_or(q >> 8, 0x000F000Fu, MAGIC);
+          const uint32_t b3 = and_or(q >> 12, 0x000F000Fu, MAGIC);
+#pragma unroll
+          for (int m = 0; m < MR; ++m) {
+            const uint4 xp = xpairs[m * RS + ks * 4 + w];
+            float &dd = d[m][w >> 1];
+            dd = dot2acc<DT>(b0, xp.x, dd);
+            dd = dot2acc<DT>(b1, xp.y, dd);
+            dd = dot2acc<DT>(b2, xp.z, dd);
+            dd = dot2acc<DT>(b3, xp.w, dd);
+          }
+        }
+        const float zf = static_cast<float>(tile_zero(cur.z, c));
+        const float s = scale_f32<SDT>(cur.s);
 #pragma unroll
         for (int m = 0; m < MR; ++m) {
-          const uint4 xp = xpairs[(m * KS4 + ks) * 4 + w];
-          float &dd = d[m][w >> 1];
-          dd = dot2acc<DT>(b0, xp.x, dd);
-          dd = dot2acc<DT>(b1, xp.y, dd);
-          dd = dot2acc<DT>(b2, xp.z, dd);
-          dd = dot2acc<DT>(b3, xp.w, dd);
+          const float2 xs = xsum[m * KS4 + ks];
+          const float v = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, (d[m][0] + d[m][1]) - xs.y), acc[m]);
+          acc[m] = valid ? v : acc[m];
         }
-      }
-      const float zf = static_cast<float>(tile_zero(cur.z, c));
-      const float s = scale_f32<SDT>(cur.s);
-#pragma unroll
-      for (int m = 0; m < MR; ++m) {
-        const float2 xs = xsum[m * KS4 + ks];
-        const float v = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, (d[m][0] + d[m][1]) - xs.y), acc[m]);
-        acc[m] = valid ? v : acc[m];
       }
       load(cur);
       cu += SW;
@@ -332,51 +445,63 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
 
   // ---- tiles of the range: waves added in order; cut tiles through the workspace ----
   const int ntl = t_last - t_first + 1;
-  const int slot = tid / (16 * MR), m = (tid >> 4) % MR, cc = tid & 15;
-  const int t = t_first + slot;
-  const int n = TILE_N * t + cc;
-  if (slot >= ntl) return;
-  float v = 0.f;
+  const int m = (tid >> 4) % MR, cc = tid & 15;
+  for (int slot = tid / (16 * MR); slot < ntl; slot += SNT / (16 * MR)) {
+    const int t = t_first + slot;
+    const int n = TILE_N * t + cc;
+    float v = 0.f;
 #pragma unroll
-  for (int w = 0; w < SW; ++w) v += red[((slot * SW + w) * MR + m) * 16 + cc];
-  const bool out_ok = m < M && n < p.N;
-  if (t * QT >= u0 && (t + 1) * QT <= u1) {  // wholly inside the range
-    if (out_ok) store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bias_at(p, n));
-    return;
-  }
-  // A cut tile: the range's first (this workgroup is its upper contributor)
-  // or its last (the lower one). Its cell: [lower workgroup][m][column].
-  const bool upper = slot == 0;
-  const int lower_b = upper ? b - 1 : b;
-  unsigned long long *cell = reinterpret_cast<unsigned long long *>(p.counters) + (lower_b * MR + m) * 16 + cc;
-  const unsigned long long mine = (1ull << 32) | __float_as_uint(v);
-  const unsigned long long old = __hip_atomic_exchange(cell, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (old >> 32) {  // the other half is in: this workgroup finishes the tile
-    const float other = __uint_as_float(static_cast<uint32_t>(old));
-    const float sum = upper ? other + v : v + other;  // lower + upper
-    if (out_ok) store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, sum + bias_at(p, n));
-    __hip_atomic_store(cell, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    for (int w = 0; w < SW; ++w) v += red[((slot * SW + w) * MR + m) * 16 + cc];
+    const bool out_ok = m < M && n < p.N;
+    if (t * QT >= u0 && (t + 1) * QT <= u1) {  // wholly inside the range
+      if (out_ok) store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bias_at(p, n));
+      continue;
+    }
+    // A cut tile: the range's first (this workgroup is its upper contributor)
+    // or its last (the lower one). Its cell: [lower workgroup][m][column].
+    const bool upper = slot == 0;
+    const int lower_b = upper ? b - 1 : b;
+    unsigned long long *cell = reinterpret_cast<unsigned long long *>(p.counters) + (lower_b * MR + m) * 16 + cc;
+    const unsigned long long mine = (1ull << 32) | __float_as_uint(v);
+    const unsigned long long old = __hip_atomic_exchange(cell, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (old >> 32) {  // the other half is in: this workgroup finishes the tile
+      const float other = __uint_as_float(static_cast<uint32_t>(old));
+      const float sum = upper ? other + v : v + other;  // lower + upper
+      if (out_ok) store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, sum + bias_at(p, n));
+      __hip_atomic_store(cell, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
 }
 
-size_t gemv_stream_lds_bytes(int MR, int KS) {
+size_t gemv_stream_lds_bytes(int MR, int KS, int nslots) {
   const size_t KS4 = static_cast<size_t>(KS + 3) / 4 * 4;
-  return static_cast<size_t>(MR) * KS4 * (4 * sizeof(uint4) + sizeof(float2)) +
-         static_cast<size_t>(SNTL) * SW * MR * 16 * sizeof(float) + 16;  // + the scatter's trash slot
+  const size_t sums = MR > 2 ? sizeof(float) : sizeof(float2), pad = MR > 2 ? sizeof(uint4) : 0;
+  return static_cast<size_t>(MR) * (KS4 * (4 * sizeof(uint4) + sums) + pad) +
+         static_cast<size_t>(nslots) * SW * MR * 16 * sizeof(float) + 16;  // + the scatter's trash slot
 }
 
 int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
   static const int wpc = std::max(1, env_int("ONECOMP_HIP_STREAM_WPC", 1));  // tuning only
-  if (M < 1 || M > 2) return 0;
-  if (gemv_stream_lds_bytes(M, KS) > 160 * 1024 - 64) return 0;
+  const int MR = M >= 1 ? stream_rows(M) : 0;
+  if (MR == 0) return 0;
   const int64_t tiles = (N + TILE_N - 1) / TILE_N, QT = (KS + 3) / 4;
-  const int64_t nwg = static_cast<int64_t>(cus) * wpc;
+  int64_t nwg = static_cast<int64_t>(cus) * wpc;
+  // The MFMA form also runs narrow layers, one workgroup per tile.
+  if (MR > 2) nwg = std::min(nwg, tiles);
   // At least a tile per workgroup (a cut tile then has two contributors), at
-  // most SNTL tiles touched by a range, and a swap cell per cut value.
+  // most SNTL tiles touched by a range, the activation rows and tile slots
+  // in LDS, and a swap cell per cut value.
   if (tiles < nwg) return 0;
+  // Staging pays off when a workgroup streams at least half as many weight
+  // bytes as it stages activation bytes (measured: M = 16, K = N = 4096, one
+  // tile per workgroup, stages 128 KB for 32 KB of weights and loses to the
+  // whole-tile kernel, which reads its activations in the stream).
+  if (MR > 2 && tiles * QT / nwg * 1024 < static_cast<int64_t>(MR) * KS * 32) return 0;
   const int64_t q1 = tiles * QT / nwg + 1;  // longest range, in units
   if ((q1 + QT - 1) / QT + 1 > SNTL) return 0;
-  if (static_cast<size_t>(nwg) * M * 16 * sizeof(unsigned long long) > cell_bytes) return 0;
+  const int nslots = stream_slots(tiles, static_cast<int>(QT), static_cast<int>(nwg));
+  if (gemv_stream_lds_bytes(MR, KS, nslots) > 160 * 1024 - 64) return 0;
+  if (static_cast<size_t>(nwg) * MR * 16 * sizeof(unsigned long long) > cell_bytes) return 0;
   return static_cast<int>(nwg);
 }
 
@@ -392,7 +517,9 @@ static void launch_stream_t(const GemmParams &p, int nwg, hipStream_t s) {
                               160 * 1024 - 64);
     attr_set.fetch_or(bit, std::memory_order_relaxed);
   }
-  hipLaunchKernelGGL(kern, dim3(nwg), dim3(SNT), gemv_stream_lds_bytes(MR, p.KS), s, p);
+  GemmParams q = p;
+  q.stream_slots = stream_slots((p.N + TILE_N - 1) / TILE_N, (p.KS + 3) / 4, nwg);
+  hipLaunchKernelGGL(kern, dim3(nwg), dim3(SNT), gemv_stream_lds_bytes(MR, p.KS, q.stream_slots), s, q);
 }
 
 template <int DT, int SDT, int MR, int SX>
@@ -411,8 +538,13 @@ static void launch_stream_x(const GemmParams &p, int nwg, hipStream_t s) {
 
 template <int DT, int SDT>
 static void launch_stream_m(const GemmParams &p, int nwg, hipStream_t s) {
-  if (p.M == 1) launch_stream_x<DT, SDT, 1>(p, nwg, s);
-  else launch_stream_x<DT, SDT, 2>(p, nwg, s);
+  switch (stream_rows(p.M)) {
+    case 1: launch_stream_x<DT, SDT, 1>(p, nwg, s); break;
+    case 2: launch_stream_x<DT, SDT, 2>(p, nwg, s); break;
+    case 4: launch_stream_x<DT, SDT, 4>(p, nwg, s); break;
+    case 8: launch_stream_x<DT, SDT, 8>(p, nwg, s); break;
+    default: launch_stream_x<DT, SDT, 16>(p, nwg, s); break;
+  }
 }
 
 void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s) {

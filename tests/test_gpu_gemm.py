@@ -649,3 +649,124 @@ def test_small_m_bias_all_regimes(regime, M):
     say(f"small-M bias regime={regime} M={M}")
     assert_gemm_close(_gemm_raw(mod, x.to(DEV), regime), _oracle_out(layer, x, bias=bias.float()),
                       f"regime {regime} M={M}")
+
+
+# -- stream kernel, MFMA form (3 <= M <= 16 chosen automatically when the
+# activation rows fit in LDS): one v_mfma_f32_16x16x32 per K step after a 4 x 4
+# transpose of the loaded octets across the wave's 16-lane rows. -------------
+def _uses_stream(mod, M):
+    """True when the automatic plan takes the stream kernel (its workspace is
+    exactly the counter area: no gathered activations, no partials)."""
+    from onecomp_runtime import _hip
+
+    w = mod.tiled()
+    nbytes = _hip.gemm_workspace_bytes(M, w.N, w.k_phys, w.group_rows, mod.kmap is not None, AUTO)
+    return nbytes == 512 * 1024
+
+
+@pytest.mark.parametrize("M,K,N,kind", [
+    (16, 2048, 16384, "plain"),     # 4 tiles per workgroup
+    (8, 5120, 5120, "actorder"),    # decode M=8 layers
+    (8, 5120, 17408, "actorder"),
+    (3, 160, 4104, "actorder"),     # 5 K steps, cut tiles, a ragged tile
+    (5, 96, 4096, "plain"),         # 3 K steps: lanes past the tile's end
+    (12, 1040, 16392, "gs26"),      # padded groups, a ragged tile
+    (8, 5120, 1024, "actorder"),    # 64 tiles: one workgroup per tile
+    (4, 128, 20000, "kmap"),        # gathered through kmap (no kinv)
+    (16, 2048, 8192, "gs128"),
+    (9, 64, 24576, "plain"),        # 6 tiles per workgroup
+])
+def test_stream_mfma_matches_oracle(M, K, N, kind, decode_kernel):
+    from onecomp_runtime import kernels, synthetic
+
+    decode_kernel("stream")
+    kw = dict(seed=130 + K % 97 + N % 89 + M)
+    if kind in ("actorder", "kmap"):
+        kw["act_order"] = True
+    if kind == "gs26":
+        kw["groupsize"] = 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer)
+    assert _uses_stream(mod, M)
+    x = synthetic.activations(M, K, seed=131)
+    say(f"stream mfma K={K} N={N} kind={kind} M={M}")
+    kinv = None if kind == "kmap" else mod.kinv
+    out = kernels.int4_gemm(x.to(DEV), mod.tiled(), in_features=K, kmap=mod.kmap, kinv=kinv)
+    assert_gemm_close(out, _oracle_out(layer, x), f"stream mfma K={K} N={N} {kind} M={M}")
+
+
+@pytest.mark.parametrize("kind", ["gs32_v1", "v2", "actorder", "gs26", "gs128", "fp16", "bf16_scales"])
+@pytest.mark.parametrize("M", [4, 16])
+def test_stream_mfma_one_hot_bit_exact(kind, M, decode_kernel):
+    """Factored scale and zero on the MFMA form reproduce dequantized rows exactly."""
+    from onecomp_runtime import synthetic
+
+    decode_kernel("stream")
+    K, N = 1024, 16384
+    kw = dict(seed=132)
+    dtype = torch.float16 if kind == "fp16" else torch.bfloat16
+    if kind == "v2":
+        kw["v1"] = False
+    if kind == "actorder":
+        kw["act_order"] = True
+    if kind == "gs26":
+        K, kw["groupsize"] = 1040, 26
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    if kind == "bf16_scales":
+        kw["scale_dtype"] = torch.bfloat16
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer, dtype)
+    assert _uses_stream(mod, M)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16" if dtype == torch.bfloat16 else "f16", layer.v1)
+    rng = np.random.default_rng(3)
+    for rep in range(2):
+        ks = rng.choice(K, M, replace=False)
+        x = torch.zeros((M, K), dtype=dtype)
+        x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+        say(f"stream mfma one-hot kind={kind} M={M} rep={rep}")
+        out = _gemm_raw(mod, x.to(DEV), AUTO)
+        assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
+
+
+def test_stream_mfma_deterministic_graph_and_whole_tile_agree(decode_kernel):
+    """Repeated calls and graph replays give identical bits; the whole-tile
+    MFMA kernel (stream off) computes the same products."""
+    from onecomp_runtime import synthetic
+
+    decode_kernel("stream")
+    K, N, M = 5120, 4104, 8
+    layer = synthetic.gptq_layer(K, N, seed=133, act_order=True)
+    mod16 = _module_for(layer, torch.float16)
+    assert _uses_stream(mod16, M)
+    x = synthetic.activations(M, K, seed=134, dtype=torch.float16)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(135)).to(torch.float16)
+    xd, bd = x.to(DEV), bias.to(DEV)
+    say("stream mfma fp16 + bias, repeated")
+    out = _gemm_bias_auto(mod16, xd, bd)
+    assert_gemm_close(out, _oracle_out(layer, x, "f16", bias), "stream mfma fp16 bias")
+    for rep in range(3):
+        assert torch.equal(_gemm_bias_auto(mod16, xd, bd), out), f"rep {rep} differs"
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        y = _gemm_bias_auto(mod16, xd, bd)
+    for rep in range(4):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, out), f"graph replay {rep} differs"
+        assert torch.equal(_gemm_bias_auto(mod16, xd, bd), out)
+    decode_kernel("tile")
+    assert not _uses_stream(mod16, M)
+    say("whole-tile MFMA kernel, same call")
+    tile = _gemm_bias_auto(mod16, xd, bd)
+    diff = (tile.float() - out.float()).abs().max().item()
+    assert diff <= 2e-2 * out.float().abs().max().item(), diff
+
+
+def _gemm_bias_auto(mod, x, bias):
+    from onecomp_runtime import kernels
+
+    return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, kinv=mod.kinv, bias=bias)

@@ -173,3 +173,25 @@ def test_loader_rejects_checkpoint_without_metadata(tmp_path):
     save_file({"w": torch.zeros(2)}, str(path))
     with pytest.raises(ValueError, match="config_json"):
         load_int4_model(str(path), lambda cfg: torch.nn.Linear(2, 2), device="cpu")
+
+
+def test_planner_takes_stream_mfma_for_small_batches():
+    """Batches of 3..16 rows take the balanced-range kernel (its workspace is
+    exactly the 512 KB swap-cell area) when their activation rows fit in LDS
+    and the workgroup streams at least half as many weight bytes as it stages;
+    otherwise the whole-tile MFMA kernel (no workspace, or gathered rows)."""
+    from onecomp_runtime import _hip
+
+    f = _hip.lib().oc_int4_gemm_workspace_bytes
+    cells = 512 * 1024
+    # (M, K_phys, N, has_kmap) -> stream?
+    cases = {
+        (8, 5120, 5120, 1): True, (8, 5120, 17408, 1): True, (8, 5120, 1024, 1): True,
+        (4, 5120, 17408, 0): True, (16, 2048, 16384, 0): True,
+        (8, 17408, 5120, 1): False,   # 8 rows of K = 17408 exceed LDS
+        (16, 4096, 4096, 0): False,   # 128 KB staged for 32 KB of weights per workgroup
+        (17, 1024, 16384, 0): False,  # beyond 16 rows
+    }
+    for (M, K, N, kmap), stream in cases.items():
+        nbytes = f(M, N, K, 32, kmap, 0)
+        assert (nbytes == cells) == stream, (M, K, N, kmap, nbytes)
