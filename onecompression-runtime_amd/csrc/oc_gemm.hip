@@ -274,78 +274,91 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 // j: MFMA j's K dimension runs over octet j of the 4 K steps, and the A
 // operand of lane (quad, r) is x[r, 32*(4qs + quad) + 8j .. +7] to match. One
 // group parameter per lane covers 32 weights.
-template <int DT, int SDT, int MT, int NW>
+template <int DT, int SDT, int MT, int NW, int PF>
 __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemmParams p) {
-  // NW waves split the tile's K. Quad-steps in flight per wave: weights and
-  // the matching activations travel together (the activations are L2 hits,
-  // but only as early as the weights can they hide their latency).
-  constexpr int PF = MT == 1 ? 3 : 2;
+  // NW waves split the tile's K; PF quad-steps in flight per wave (weights
+  // and the matching activations travel together: the activations are L2
+  // hits, but only as early as the weights can they hide their latency).
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int t = xcd_block(blockIdx.x, gridDim.x);
   const int n = TILE_N * t + c16;
   const int KS = p.KS, M = p.M;
   const int QS = (KS + 3) / 4;
-  const uint4 *qt4 = static_cast<const uint4 *>(p.qw) + static_cast<int64_t>(t) * KS * TILE_N + c16;
-  const uint16_t *stp = static_cast<const uint16_t *>(p.scales) + static_cast<int64_t>(t) * p.G * TILE_N + c16;
-  const uint32_t *ztp = static_cast<const uint32_t *>(p.zeros) + static_cast<int64_t>(t) * p.G * 2 + (c16 >> 3);
-  const uint16_t *a = static_cast<const uint16_t *>(p.a);
+  // Branch-free buffer loads (a branch around a load made the compiler wait
+  // for it before issuing the next): steps past KS and rows past M read an
+  // offset beyond every buffer, which returns zeros without a memory access;
+  // zero codes, scales and activations then add exactly zero.
+  const int tiles = (p.N + TILE_N - 1) / TILE_N;
+  const __amdgpu_buffer_rsrc_t q_rs = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
+  const __amdgpu_buffer_rsrc_t s_rs = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * p.G * 32);
+  const __amdgpu_buffer_rsrc_t z_rs = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * p.G * 8);
+  const __amdgpu_buffer_rsrc_t a_rs = buffer_rsrc(p.a, p.a_bytes);  // host: a_bytes < 2^31
+  constexpr uint32_t NOWHERE = 0xFFFFF000u;
+  const uint32_t q_base = (static_cast<uint32_t>(t) * KS * TILE_N + c16) * 16u;  // + 256 ks
+  const uint32_t s_base = (static_cast<uint32_t>(t) * p.G * TILE_N + c16) * 2u;  // + 32 g
+  const uint32_t z_base = (static_cast<uint32_t>(t) * p.G * 2 + (c16 >> 3)) * 4u;  // + 8 g
+  uint32_t a_row[MT];  // byte offset of activation row 16 tt + c16, NOWHERE past M
+#pragma unroll
+  for (int tt = 0; tt < MT; ++tt) {
+    const int row = 16 * tt + c16;
+    a_row[tt] = row < M ? static_cast<uint32_t>(row * p.lda * 2) : NOWHERE;
+  }
 
   struct Stage {
     uint4 q;
     uint32_t s;
     uint32_t z;
-    uint4 x[MT][4];
+    uint32_t x[MT][16];  // 4 chunks of 16 bytes per row tile (flat: stays in registers)
   };
   Stage st[PF];
-  auto load = [&](Stage &S, int qs) {
+  auto load = [&](Stage &S, int qs) __attribute__((always_inline)) {
     const int ks = 4 * qs + quad;
     const bool kin = ks < KS;
-    if (kin) {
-      S.q = qt4[ks * TILE_N];
-      const int g = group_of(p, ks);
-      S.s = stp[g * TILE_N];
-      S.z = ztp[g * 2];
-    } else {
-      S.q = make_uint4(0, 0, 0, 0);
-      S.s = 0;
-      S.z = 0;
-    }
+    const uint32_t g = static_cast<uint32_t>(group_of(p, kin ? ks : 0));
+    const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, kin ? q_base + 256u * ks : NOWHERE, 0, 0);
+    S.q = make_uint4(q[0], q[1], q[2], q[3]);
+    S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, kin ? s_base + 32u * g : NOWHERE, 0, 0);
+    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, kin ? z_base + 8u * g : NOWHERE, 0, 0);
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) {
-      const int row = 16 * tt + c16;
-      const bool ok = row < M && kin;
-      const uint16_t *src = a + static_cast<int64_t>(row) * p.lda + 32 * ks;
+      const uint32_t off = kin && a_row[tt] != NOWHERE ? a_row[tt] + 64u * ks : NOWHERE;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-        S.x[tt][j] = ok ? *reinterpret_cast<const uint4 *>(src + 8 * j) : make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < 4; ++j) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(a_rs, off == NOWHERE ? NOWHERE : off + 16u * j, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S.x[tt][4 * j + e] = v[e];
+      }
     }
   };
-#pragma unroll
-  for (int f = 0; f < PF; ++f) {
-    const int qs = wave + NW * f;
-    if (qs < QS) load(st[f], qs);
-  }
+  // Quad-steps of this wave: wave, wave + NW, ...; the count is padded to
+  // whole rounds of PF (the padding reads zeros).
+  const int nq = wave < QS ? (QS - wave + NW - 1) / NW : 0;
+  const int nq_pad = (nq + PF - 1) / PF * PF;
+  static_for<0, PF>([&](auto F) __attribute__((always_inline)) {
+    load(st[F], wave + NW * F);
+    __builtin_amdgcn_sched_barrier(0);
+  });
   v4f32 acc[MT];
 #pragma unroll
   for (int tt = 0; tt < MT; ++tt) acc[tt] = v4f32{0.f, 0.f, 0.f, 0.f};
 
-  for (int base = wave; base < QS; base += NW * PF) {
-#pragma unroll
-    for (int f = 0; f < PF; ++f) {
-      const int qs = base + NW * f;
-      if (qs >= QS) break;
-      const Stage cur = st[f];
-      if (qs + NW * PF < QS) load(st[f], qs + NW * PF);
+  for (int i0 = 0; i0 < nq_pad; i0 += PF) {
+    static_for<0, PF>([&](auto F) __attribute__((always_inline)) {
+      Stage &cur = st[F];  // consumed, then refilled in place
       const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c16));
       const uint32_t qwords[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint4 b = dequant8<DT>(qwords[j], gp);
 #pragma unroll
-        for (int tt = 0; tt < MT; ++tt) acc[tt] = mfma16x16x32<DT>(cur.x[tt][j], b, acc[tt]);
+        for (int tt = 0; tt < MT; ++tt) {
+          const uint4 xa = make_uint4(cur.x[tt][4 * j], cur.x[tt][4 * j + 1], cur.x[tt][4 * j + 2], cur.x[tt][4 * j + 3]);
+          acc[tt] = mfma16x16x32<DT>(xa, b, acc[tt]);
+        }
       }
-    }
+      load(cur, wave + NW * (i0 + F + PF));
+    });
   }
 
   // acc[tt][i] = row 16tt + 4*quad + i, column c16. Fixed LDS tree over the NW waves.
@@ -1162,8 +1175,13 @@ void launch_dot(const GemmParams &p, const Plan &sp, hipStream_t s) {
 
 template <int DT, int SDT, int MT, int NW>
 void launch_mfma_t(const GemmParams &p, hipStream_t s) {
-  hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT, NW>), dim3((p.N + TILE_N - 1) / TILE_N), dim3(64 * NW), 0, s,
-                     p);
+  // Quad-steps in flight (measured on MI355X): one when a wave has at most 4
+  // (K = N = 4096, M = 16: 7.6 vs 8.2 us with 2 or 3), else two (K = 17408,
+  // M = 8: 31.9 vs 34.5 us with one).
+  const int per_wave = ((p.KS + 3) / 4 + NW - 1) / NW;
+  const dim3 grid((p.N + TILE_N - 1) / TILE_N), block(64 * NW);
+  if (per_wave <= 4) hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT, NW, 1>), grid, block, 0, s, p);
+  else hipLaunchKernelGGL((gemv_mfma_kernel<DT, SDT, MT, NW, 2>), grid, block, 0, s, p);
 }
 
 template <int DT, int SDT, int MT>
@@ -1338,6 +1356,10 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
     p.lda = K_phys;
   }
   p.a_bytes = (static_cast<int64_t>(M) - 1) * p.lda * 2 + static_cast<int64_t>(sp.gather ? K_phys : K_logical) * 2;
+  // The whole-tile MFMA kernel addresses activation rows with 32-bit offsets.
+  if (sp.regime == OC_REGIME_SPLITK && sp.stream_wgs == 0 && p.a_bytes >= (int64_t{1} << 31))
+    return fail(OC_ERR_SHAPE, "activation rows span %lld bytes (2 GiB or more): pass a compact copy",
+                static_cast<long long>(p.a_bytes));
   if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(ws_after_counters + gather_bytes(sp, M, K_phys));
   p.kmap = kmap;
   p.counters = need > 0 ? static_cast<int *>(workspace) : nullptr;

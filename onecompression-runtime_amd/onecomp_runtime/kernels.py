@@ -192,8 +192,10 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
     adt = a_2d.dtype
     if adt is not torch.bfloat16 and adt is not torch.float16:
         raise ValueError(f"activations must be fp16 or bf16, got {adt}")
-    if a_2d.stride(-1) != 1 or a_2d.stride(0) % 8 or a_2d.data_ptr() % 16:
-        # The kernels read 16-byte row segments: copy into rows padded to 8.
+    if (a_2d.stride(-1) != 1 or a_2d.stride(0) % 8 or a_2d.data_ptr() % 16
+            or (a_2d.shape[0] - 1) * a_2d.stride(0) + a_2d.shape[1] >= 1 << 30):
+        # The kernels read 16-byte row segments (and address a block of rows
+        # below 2 GiB with 32-bit offsets): copy into compact rows padded to 8.
         K = a_2d.shape[1]
         buf = torch.empty((a_2d.shape[0], (K + 7) // 8 * 8), dtype=adt, device=a_2d.device)
         a_2d = buf[:, :K].copy_(a_2d)
