@@ -144,11 +144,13 @@ def test_gemm_dequant_bit_exact_one_hot(regime, kind):
     assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, dtype))
 
 
-@pytest.mark.parametrize("M,K,N,kind", [(256, 1024, 192, "gs32_v1"), (300, 2048, 400, "actorder"),
-                                         (512, 1040, 96, "gs26"), (257, 4096, 64, "v2"), (600, 512, 1000, "gs128")])
+@pytest.mark.parametrize("M,K,N,kind", [(512, 1024, 192, "gs32_v1"), (600, 2048, 400, "actorder"),
+                                         (512, 1040, 96, "gs26"), (513, 4096, 64, "v2"), (600, 512, 1000, "gs128"),
+                                         (256, 1024, 192, "gs32_v1"), (300, 2048, 400, "actorder")])
 def test_large_m_kernel_one_hot_bit_exact(M, K, N, kind):
-    """The pipelined large-M kernel (M >= 256; split K when the grid is small)
-    reproduces dequantized columns exactly."""
+    """The pipelined 128 x 192 kernel (512 <= M < 1024; split K when the grid
+    is small) and, below 512 rows, the tiled kernel reproduce dequantized
+    columns exactly."""
     from onecomp_runtime import synthetic
 
     kw = dict(seed=33)
