@@ -878,50 +878,93 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void g
 // One workgroup of 256 threads; thread t owns the contiguous pair range
 // [t*per, (t+1)*per), so ranks computed from per-thread prefix counts keep
 // the original pair order inside every expert.
-constexpr int ROUTE_THREADS = 256;
+constexpr int ROUTE_WAVES = 16;
+constexpr int ROUTE_THREADS = 64 * ROUTE_WAVES;
 
+// Stable counting sort of the P = T * topk (token, slot) pairs by expert, in
+// one workgroup. Wave w owns the pairs [w * chunk, (w + 1) * chunk), 64 at a
+// time: the lanes of a batch that hold the same expert find each other with
+// one ballot per expert-id bit, so a lane's rank among them is a popcount
+// and the highest of them adds the batch's count to the wave's counter for
+// that expert (no atomics; pair order is kept within and across batches).
+// Expert totals, their exclusive scan (offsets) and per-wave bases follow;
+// a second pass writes every pair at base + rank. Ids outside [0, E) are
+// dropped.
 __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const int64_t *__restrict__ ids, int P,
                                                                   int E, int32_t *__restrict__ offsets,
                                                                   int32_t *__restrict__ sorted) {
-  extern __shared__ int32_t cnt[];  // [ROUTE_THREADS + 1][E]: per-thread counts, then totals
-  const int tid = threadIdx.x;
-  const int per = (P + ROUTE_THREADS - 1) / ROUTE_THREADS;
-  const int p_begin = min(tid * per, P), p_end = min(p_begin + per, P);
-  for (int e = tid; e < (ROUTE_THREADS + 1) * E; e += ROUTE_THREADS) cnt[e] = 0;
+  extern __shared__ int32_t cnt[];  // [ROUTE_WAVES][E] per-wave counts (then bases), then [E] offsets
+  __shared__ int32_t wave_tot[ROUTE_WAVES];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int32_t *eoff = cnt + ROUTE_WAVES * E;
+  const int bits = 32 - __builtin_clz(static_cast<unsigned>(E));  // ids 0..E (E marks "dropped")
+  const int chunk = (P + ROUTE_WAVES - 1) / ROUTE_WAVES;
+  const int q_begin = min(w * chunk, P), q_end = min(q_begin + chunk, P);
+  const uint64_t below = (uint64_t{1} << lane) - 1;
+  for (int i = tid; i < (ROUTE_WAVES + 1) * E; i += ROUTE_THREADS) cnt[i] = 0;
   __syncthreads();
-  for (int q = p_begin; q < p_end; ++q) {
-    const int64_t e = ids[q];
-    if (e >= 0 && e < E) ++cnt[tid * E + e];
+
+  // Same-expert lanes of a batch, this lane's rank among them and their count.
+  auto match = [&](int q, int &e, int &rank, int &count) {
+    int64_t id = q < q_end ? ids[q] : -1;
+    e = id >= 0 && id < E ? static_cast<int>(id) : E;
+    uint64_t mask = __ballot(1);
+    for (int b = 0; b < bits; ++b) {
+      const uint64_t bb = __ballot((e >> b) & 1);
+      mask &= ((e >> b) & 1) ? bb : ~bb;
+    }
+    rank = __popcll(mask & below);
+    count = __popcll(mask);
+  };
+  int32_t *wc = cnt + w * E;
+  for (int q0 = q_begin; q0 < q_end; q0 += 64) {
+    int e, rank, count;
+    match(q0 + lane, e, rank, count);
+    if (e < E && rank == count - 1) wc[e] += count;
   }
   __syncthreads();
-  // Exclusive prefix over threads for each expert (expert e handled by thread e % 256).
-  for (int e = tid; e < E; e += ROUTE_THREADS) {
-    int run = 0;
-    for (int t = 0; t < ROUTE_THREADS; ++t) {
-      const int c = cnt[t * E + e];
-      cnt[t * E + e] = run;
+
+  // Expert totals, exclusive scan over experts (E <= ROUTE_THREADS: a scan
+  // per wave, then over the wave totals).
+  {
+    const int e = tid;
+    int tot = 0;
+    if (e < E)
+      for (int v = 0; v < ROUTE_WAVES; ++v) tot += cnt[v * E + e];
+    int incl = tot;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int up = __shfl_up(incl, d);
+      if (lane >= d) incl += up;
+    }
+    if (lane == 63) wave_tot[w] = incl;
+    __syncthreads();
+    int before = 0;
+    for (int v = 0; v < w; ++v) before += wave_tot[v];
+    if (e < E) eoff[e] = before + incl - tot;  // exclusive offset of expert e
+    __syncthreads();
+  }
+  // Per-wave bases: offset of the expert plus the counts of earlier waves.
+  if (tid < E) {
+    const int e = tid;
+    offsets[e] = eoff[e];
+    int run = eoff[e];
+    for (int v = 0; v < ROUTE_WAVES; ++v) {
+      const int c = cnt[v * E + e];
+      cnt[v * E + e] = run;
       run += c;
     }
-    cnt[ROUTE_THREADS * E + e] = run;
+    if (e == E - 1) offsets[E] = run;  // pairs kept
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < E; ++e) {
-      offsets[e] = run;
-      const int c = cnt[ROUTE_THREADS * E + e];
-      cnt[ROUTE_THREADS * E + e] = run;
-      run += c;
-    }
-    offsets[E] = run;
-  }
-  __syncthreads();
-  for (int q = p_begin; q < p_end; ++q) {
-    const int64_t e = ids[q];
-    if (e >= 0 && e < E) {
-      const int pos = cnt[ROUTE_THREADS * E + e] + cnt[tid * E + e]++;
-      sorted[pos] = q;
-    }
+
+  for (int q0 = q_begin; q0 < q_end; q0 += 64) {
+    int e, rank, count;
+    match(q0 + lane, e, rank, count);
+    // Every lane reads its base before the group's last lane advances it
+    // (one wave's LDS accesses complete in program order).
+    const int base = e < E ? wc[e] : 0;
+    if (e < E) sorted[base + rank] = q0 + lane;
+    if (e < E && rank == count - 1) wc[e] = base + count;
   }
 }
 
@@ -1444,8 +1487,8 @@ int oc_moe_route(const int64_t *topk_ids, int32_t T, int32_t topk, int32_t E, in
   if (!topk_ids || !expert_offsets || !sorted_pairs) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
   if (T < 0 || topk <= 0 || E <= 0 || E > 1024 || static_cast<int64_t>(T) * topk > 65536)
     return fail(OC_ERR_SHAPE, "unsupported routing shape T=%d topk=%d E=%d", T, topk, E);
-  const size_t lds = sizeof(int32_t) * (ROUTE_THREADS + 1) * E;
-  if (lds > 160 * 1024) return fail(OC_ERR_UNSUPPORTED, "too many experts for one workgroup (E=%d)", E);
+  const size_t lds = sizeof(int32_t) * (ROUTE_WAVES + 1) * E;
+  if (lds > 128 * 1024) return fail(OC_ERR_UNSUPPORTED, "too many experts for one workgroup (E=%d)", E);
   if (lds > 64 * 1024)
     (void)hipFuncSetAttribute(reinterpret_cast<const void *>(moe_route_kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));

@@ -138,6 +138,32 @@ def test_moe_route_drops_invalid_ids():
     assert pairs.cpu().tolist()[:4] == [0, 1, 4, 5]
 
 
+@pytest.mark.parametrize("T,topk,E,kind", [(512, 8, 64, "skewed"), (8192, 8, 1024, "uniform"),
+                                            (300, 3, 100, "invalid"), (77, 1, 1, "uniform"),
+                                            (1000, 5, 33, "invalid")])
+def test_moe_route_stable_sort_shapes(T, topk, E, kind):
+    """Ranks of same-expert pairs within 64-pair batches, per-wave counters
+    and the expert scan give numpy's stable order; ids outside [0, E) drop."""
+    from onecomp_runtime import kernels
+
+    rng = np.random.default_rng(T + E)
+    if kind == "skewed":  # most pairs on two experts
+        flat = np.where(rng.random(T * topk) < 0.9, rng.integers(0, 2, T * topk), rng.integers(0, E, T * topk))
+    else:
+        flat = rng.integers(0, E, T * topk)
+    if kind == "invalid":
+        bad = rng.random(T * topk) < 0.2
+        flat = np.where(bad, rng.choice([-1, E, E + 5], T * topk), flat)
+    ids = torch.from_numpy(flat.reshape(T, topk).astype(np.int64))
+    say(f"moe route T={T} topk={topk} E={E} {kind}")
+    off, pairs = kernels.moe_route(ids.to(DEV), E)
+    valid = (flat >= 0) & (flat < E)
+    order = np.argsort(np.where(valid, flat, E), kind="stable")[: int(valid.sum())]
+    counts = np.bincount(flat[valid], minlength=E)
+    assert np.array_equal(off.cpu().numpy(), np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(pairs.cpu().numpy()[: int(valid.sum())], order)
+
+
 @pytest.mark.parametrize("E,K,N,T,topk", [(64, 4096, 2048, 512, 8), (8, 512, 256, 37, 2)])
 def test_moe_grouped_gemm(E, K, N, T, topk):
     from onecomp_runtime import kernels, synthetic
