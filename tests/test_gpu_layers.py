@@ -73,21 +73,23 @@ def test_rtn_linear_bias_and_fp32_path():
 
 
 @pytest.mark.parametrize("G", [1, 32])
-@pytest.mark.parametrize("scale_dtype", [torch.float16, torch.bfloat16])
-def test_embedding_workload_bit_exact(G, scale_dtype):
+@pytest.mark.parametrize("scale_dtype,zero_dtype", [(torch.float16, torch.float16),
+                                                    (torch.bfloat16, torch.float16),
+                                                    (torch.bfloat16, torch.bfloat16)])
+def test_embedding_workload_bit_exact(G, scale_dtype, zero_dtype):
     from onecomp_runtime import PackedEmbedding, synthetic
 
     V, D, T = 32768, 1024, 4096
     layer = synthetic.rtn_layer(V, D, seed=20310, groups=G)
-    scales = layer.scales.to(scale_dtype)
+    scales, zeros = layer.scales.to(scale_dtype), layer.zeros.to(zero_dtype)
     ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311))
-    emb = PackedEmbedding(V, D, layer.qweight_u8.to(DEV), scales.to(DEV), layer.zeros.to(DEV))
-    say(f"embedding G={G} scales={scale_dtype}")
+    emb = PackedEmbedding(V, D, layer.qweight_u8.to(DEV), scales.to(DEV), zeros.to(DEV))
+    say(f"embedding G={G} scales={scale_dtype} zeros={zero_dtype}")
     out = emb(ids.to(DEV))
     assert out.dtype == scale_dtype and out.shape == (T, D)
     fmt = "bf16" if scale_dtype == torch.bfloat16 else "f16"
     ref = O.embedding(ids.numpy(), layer.qweight_u8.numpy(), scales.float().numpy(),
-                      layer.zeros.float().numpy(), D, fmt)
+                      zeros.float().numpy(), D, fmt)
     assert np.array_equal(bits16(out), oracle_bits(ref, scale_dtype))
 
 
