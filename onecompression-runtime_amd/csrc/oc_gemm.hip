@@ -1005,6 +1005,7 @@ struct Plan {
   bool legacy_dot;  // decode: whole-tile gemv_dot_kernel (else the split-item GEMV)
   GemvPlan gv;      // decode: split GEMV work items
   int stream_wgs;   // decode: balanced-range GEMV with this many workgroups (0: not used)
+  bool stream_global;  // ... reading gathered activation rows from global memory
 };
 
 // Workspace layout, every regime: [counter area][gathered activations][fp32
@@ -1120,10 +1121,18 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     // (read per call) keeps them on the whole-tile MFMA kernel below.
     if (automatic && M >= 3 && M <= 16 && ilog2_exact(group_rows / 32) >= 0 &&
         env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
-      sp.stream_wgs = gemv_stream_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
+      // ONECOMP_HIP_STREAM_GLOBAL=1 (read per call; tests) skips the staged form.
+      const bool global_only = env_int("ONECOMP_HIP_STREAM_GLOBAL", 0) != 0;
+      sp.stream_wgs = global_only ? 0 : gemv_stream_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
       if (sp.stream_wgs > 0) {
         sp.gather = false;
         return sp;
+      }
+      // Rows beyond LDS: the same ranges over gathered rows in global memory.
+      sp.stream_wgs = gemv_stream_global_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
+      if (sp.stream_wgs > 0) {
+        sp.stream_global = true;
+        return sp;  // sp.gather as planned: act-order rows are gathered first
       }
     }
     sp.mt = std::max(1, (M + 15) / 16);
@@ -1387,7 +1396,7 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   p.G = K_phys / group_rows;
   p.group_rows = group_rows;
   p.gshift = ilog2_exact(group_rows / 32);
-  p.kinv = (sp.regime == OC_REGIME_DOT || sp.stream_wgs > 0) && kmap ? kinv : nullptr;
+  p.kinv = (sp.regime == OC_REGIME_DOT || (sp.stream_wgs > 0 && !sp.stream_global)) && kmap ? kinv : nullptr;
   p.bias = bias;
   p.bias_dtype = bias_dtype;
   p.c = c;
@@ -1402,14 +1411,14 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   }
   p.a_bytes = (static_cast<int64_t>(M) - 1) * p.lda * 2 + static_cast<int64_t>(sp.gather ? K_phys : K_logical) * 2;
   // The whole-tile MFMA kernel addresses activation rows with 32-bit offsets.
-  if (sp.regime == OC_REGIME_SPLITK && sp.stream_wgs == 0 && p.a_bytes >= (int64_t{1} << 31))
+  if (sp.regime == OC_REGIME_SPLITK && (sp.stream_wgs == 0 || sp.stream_global) && p.a_bytes >= (int64_t{1} << 31))
     return fail(OC_ERR_SHAPE, "activation rows span %lld bytes (2 GiB or more): pass a compact copy",
                 static_cast<long long>(p.a_bytes));
   if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(ws_after_counters + gather_bytes(sp, M, K_phys));
   p.kmap = kmap;
   p.counters = need > 0 ? static_cast<int *>(workspace) : nullptr;
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (sp.stream_wgs > 0) launch_gptq_gemv_stream(p, a_dtype, scale_dtype, sp.stream_wgs, s);
+  if (sp.stream_wgs > 0) launch_gptq_gemv_stream(p, a_dtype, scale_dtype, sp.stream_wgs, sp.stream_global, s);
   else if (sp.regime == OC_REGIME_DOT && !sp.legacy_dot) launch_gptq_gemv(p, a_dtype, scale_dtype, sp.gv.T, s);
   else if (sp.wide_wn) launch_gptq_wide(p, a_dtype, scale_dtype, sp.wide_wn, s);
   else if (bf && sbf) launch_gptq<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, sp, s);

@@ -205,6 +205,10 @@ void launch_gptq_gemv(const GemmParams &p, int a_dtype, int scale_dtype, int T, 
 // cell_bytes hold). The launch needs p.counters: nwg * MR * 16 zeroed 64-bit
 // cells (MR = M rounded up to 1, 2, 4, 8 or 16), left zero.
 int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
-void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s);
+// The same ranges for 3..16 rows read from global memory in physical row order
+// (no staging; for rows beyond LDS when whole tiles would load CUs unevenly).
+int gemv_stream_global_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
+void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, bool global_rows,
+                             hipStream_t s);
 
 }  // namespace oc

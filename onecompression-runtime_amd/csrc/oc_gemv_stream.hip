@@ -58,7 +58,10 @@ constexpr int SW = 16;        // waves per workgroup
 constexpr int SNT = 64 * SW;  // threads per workgroup
 constexpr int SNTL = 8;       // tiles one workgroup's range may touch
 
-enum { SX_CONTIG = 0, SX_SCATTER = 1, SX_GATHER = 2 };
+// Activation rows: staged into LDS (copied, scattered through kinv, gathered
+// through kmap), or read from global memory per unit (SX_GLOBAL: rows already
+// in physical order; MFMA form with exact dequantization).
+enum { SX_CONTIG = 0, SX_SCATTER = 1, SX_GATHER = 2, SX_GLOBAL = 3 };
 
 // Balanced ranges: U = nwg q + r units; workgroups b < r own q + 1 units,
 // the others q (q >= QT: the host launches at most one workgroup per tile).
@@ -86,8 +89,10 @@ template <int DT, int SDT, int MR, int SX, int PF, bool AL>
 __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
   constexpr bool MF = MR > 2;     // MFMA inner product (rows 4 g + i of lane (g, c))
+  constexpr bool GL = SX == SX_GLOBAL;  // activations from global memory, nothing staged
   constexpr int SB = MF ? 1 : 3;  // staged octets per thread per batch
   static_assert(!MF || MR == 4 || MR == 8 || MR == 16, "MFMA rows");
+  static_assert(!GL || MF, "global activation rows take the MFMA form");
   extern __shared__ __attribute__((aligned(16))) uint4 sx_lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -103,11 +108,11 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   const int nslots = p.stream_slots;                                 // tiles a range touches, at most
   // Row stride of the staged pairs, in 16-byte chunks: the MFMA form reads
   // 16 rows at once and pads each row by one chunk (distinct banks).
-  const int RS = 4 * KS4 + (MF ? 1 : 0);
+  const int RS = GL ? 0 : 4 * KS4 + (MF ? 1 : 0);
   uint4 *xpairs = sx_lds;                                          // [MR][RS]
   float2 *xsum = reinterpret_cast<float2 *>(sx_lds + MR * RS);  // dot2: [MR][KS4] (sum, B * sum)
   float *xst = reinterpret_cast<float *>(sx_lds + MR * RS);     // MFMA: [KS4][MR] sums
-  float *red = MF ? xst + KS4 * MR : reinterpret_cast<float *>(xsum + MR * KS4);  // [nslots][SW][MR][16]
+  float *red = MF ? xst + (GL ? 0 : KS4 * MR) : reinterpret_cast<float *>(xsum + MR * KS4);  // [nslots][SW][MR][16]
   // 16-bit slot that takes the scatter's writes for rows without a place.
   const int trash16 = static_cast<int>(reinterpret_cast<uint16_t *>(red + nslots * SW * MR * 16) -
                                        reinterpret_cast<uint16_t *>(xpairs));
@@ -120,7 +125,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   // ---- activation staging, batch by batch; the weight stream starts after
   // the first batch's loads so both are in flight together ----
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
-  const int n_items = SX == SX_SCATTER ? (p.K_logical >> 3) : KS * 4;  // octets to stage
+  const int n_items = GL ? 0 : SX == SX_SCATTER ? (p.K_logical >> 3) : KS * 4;  // octets to stage
   const uint4 *kinv4 = reinterpret_cast<const uint4 *>(p.kinv);
   uint4 xr[MR][SB];
   uint4 rr[SB];
@@ -212,11 +217,13 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   // padding steps [KS, KS4) of every row (a unit's lanes past the last K
   // step multiply zeros).
   for (int i = tid; i < nslots * SW * MR * 16; i += SNT) red[i] = 0.f;
-  const int pad = 4 * (KS4 - KS);
-  for (int i = tid; i < MR * pad; i += SNT) {
-    const int m = i / pad, j = i - m * pad;
-    xpairs[m * RS + KS * 4 + j] = make_uint4(0, 0, 0, 0);
-    if (j < KS4 - KS) put_sum(m, KS + j, 0.f);
+  if constexpr (!GL) {
+    const int pad = 4 * (KS4 - KS);
+    for (int i = tid; i < MR * pad; i += SNT) {
+      const int m = i / pad, j = i - m * pad;
+      xpairs[m * RS + KS * 4 + j] = make_uint4(0, 0, 0, 0);
+      if (j < KS4 - KS) put_sum(m, KS + j, 0.f);
+    }
   }
   if constexpr (SX == SX_SCATTER) {
     if (p.K_logical != p.K_phys) {  // physical rows without a source stay zero
@@ -248,7 +255,15 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     uint32_t s[4];
     uint32_t z;
   };
-  using Stage = std::conditional_t<MF, StageMf, StageDot>;
+  // Global form: the dot2 form's weight loads plus the A operand of lane
+  // (h, r): row r's 32 activations of K step 4 q + h (four 16-byte loads).
+  struct StageGl {
+    uint4 q;
+    uint32_t s;
+    uint32_t z;
+    uint32_t x[16];
+  };
+  using Stage = std::conditional_t<GL, StageGl, std::conditional_t<MF, StageMf, StageDot>>;
   // Buffer loads: a wave-uniform unit offset plus a fixed per-lane offset.
   // Lanes past a tile's last K step read the next tile (or past the end:
   // zero), which meets the zero padding of the staged activations; units
@@ -258,9 +273,13 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   const __amdgpu_buffer_rsrc_t q_rs = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
   const __amdgpu_buffer_rsrc_t s_rs = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * G * 32);
   const __amdgpu_buffer_rsrc_t z_rs = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * G * 8);
-  const uint32_t q_lane = MF ? static_cast<uint32_t>(c * 16 + 4 * h) : lane * 16u;  // + 256 j (MFMA form)
-  const uint32_t s_lane = MF ? static_cast<uint32_t>(c) * 2u                          // + 32 (j >> gs2)
-                             : static_cast<uint32_t>((h >> gs2) * 16 + c) * 2u;      // group of K step 4 q + h
+  constexpr bool MFL = MF && !GL;  // per-octet weight loads (staged MFMA form)
+  const uint32_t q_lane = MFL ? static_cast<uint32_t>(c * 16 + 4 * h) : lane * 16u;  // + 256 j (MFMA form)
+  const uint32_t s_lane = MFL ? static_cast<uint32_t>(c) * 2u                          // + 32 (j >> gs2)
+                              : static_cast<uint32_t>((h >> gs2) * 16 + c) * 2u;      // group of K step 4 q + h
+  // Global form: row c of the activations (rows past M read nowhere).
+  const __amdgpu_buffer_rsrc_t a_rs = buffer_rsrc(p.a, GL ? p.a_bytes : 0);
+  const uint32_t a_row = GL && c < M ? static_cast<uint32_t>(c * p.lda * 2) : 0xFFFFF000u;
   const uint32_t z_lane = static_cast<uint32_t>((h >> gs2) * 2 + (c >> 3)) * 4u;
   constexpr uint32_t NOWHERE = 0xFFFFF000u;
   const int w_u0 = u0 + wave;  // this wave's first unit; it takes every SW-th from there
@@ -277,7 +296,19 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     }
     const bool in = pu < u1;
     const uint32_t qo = q_lane + (in ? qb : NOWHERE), so = s_lane + (in ? gb * 32u : NOWHERE);
-    if constexpr (MF) {
+    if constexpr (GL) {
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0, 0);
+      S.q = make_uint4(q[0], q[1], q[2], q[3]);
+      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0, 0);
+      const int ks = 4 * (pu % QT) + h;  // this lane's K step (steps past KS read zeros)
+      const bool a_in = in && ks < KS && a_row != NOWHERE;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(a_rs, a_in ? a_row + 64u * ks + 16u * j : NOWHERE, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) S.x[4 * j + e] = v[e];
+      }
+    } else if constexpr (MF) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         S.q[j] = __builtin_amdgcn_raw_buffer_load_b32(q_rs, qo + 256u * j, 0, 0);
@@ -367,7 +398,22 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
         cur_t = ct;
       }
       const int qq = min(cu - ct * QT, QT - 1);  // unit within the tile; K steps 4 qq .. 4 qq + 3 < KS4
-      if constexpr (MF) {
+      if constexpr (GL) {
+        // Exact dequantization (the scale inside B), so the unit's MFMAs
+        // accumulate across its four K steps: MFMA j takes word j of every
+        // lane (octet j of K step 4 qq + h) against row r's matching octet.
+        const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c));
+        const uint32_t qw[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+        v4f32 av = {acc[0], acc[1], acc[2], acc[3]};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint4 b = dequant8<DT>(qw[j], gp);
+          const uint4 xa = make_uint4(cur.x[4 * j], cur.x[4 * j + 1], cur.x[4 * j + 2], cur.x[4 * j + 3]);
+          av = mfma16x16x32<DT>(xa, b, av);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = av[i];
+      } else if constexpr (MF) {
         // LDS operands first (their latency overlaps the decode): A =
         // row c's pairs of octet h of each step (rows past MR read row
         // MR - 1 and feed output rows that are never stored), and row c's
@@ -473,11 +519,11 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   }
 }
 
-size_t gemv_stream_lds_bytes(int MR, int KS, int nslots) {
+size_t gemv_stream_lds_bytes(int MR, int KS, int nslots, bool global_rows) {
   const size_t KS4 = static_cast<size_t>(KS + 3) / 4 * 4;
   const size_t sums = MR > 2 ? sizeof(float) : sizeof(float2), pad = MR > 2 ? sizeof(uint4) : 0;
-  return static_cast<size_t>(MR) * (KS4 * (4 * sizeof(uint4) + sums) + pad) +
-         static_cast<size_t>(nslots) * SW * MR * 16 * sizeof(float) + 16;  // + the scatter's trash slot
+  const size_t staged = global_rows ? 0 : static_cast<size_t>(MR) * (KS4 * (4 * sizeof(uint4) + sums) + pad);
+  return staged + static_cast<size_t>(nslots) * SW * MR * 16 * sizeof(float) + 16;  // + the scatter's trash slot
 }
 
 int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
@@ -500,7 +546,23 @@ int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
   const int64_t q1 = tiles * QT / nwg + 1;  // longest range, in units
   if ((q1 + QT - 1) / QT + 1 > SNTL) return 0;
   const int nslots = stream_slots(tiles, static_cast<int>(QT), static_cast<int>(nwg));
-  if (gemv_stream_lds_bytes(MR, KS, nslots) > 160 * 1024 - 64) return 0;
+  if (gemv_stream_lds_bytes(MR, KS, nslots, false) > 160 * 1024 - 64) return 0;
+  if (static_cast<size_t>(nwg) * MR * 16 * sizeof(unsigned long long) > cell_bytes) return 0;
+  return static_cast<int>(nwg);
+}
+
+int gemv_stream_global_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
+  if (M < 3 || M > 16) return 0;
+  const int MR = stream_rows(M);
+  const int64_t tiles = (N + TILE_N - 1) / TILE_N, QT = (KS + 3) / 4, nwg = cus;
+  // Worth it where whole tiles would load compute units unevenly (a tile
+  // count that is not a multiple of the workgroups), with the range
+  // conditions of the staged form.
+  if (tiles < nwg || tiles % nwg == 0) return 0;
+  const int64_t q1 = tiles * QT / nwg + 1;
+  if ((q1 + QT - 1) / QT + 1 > SNTL) return 0;
+  const int nslots = stream_slots(tiles, static_cast<int>(QT), static_cast<int>(nwg));
+  if (gemv_stream_lds_bytes(MR, KS, nslots, true) > 160 * 1024 - 64) return 0;
   if (static_cast<size_t>(nwg) * MR * 16 * sizeof(unsigned long long) > cell_bytes) return 0;
   return static_cast<int>(nwg);
 }
@@ -519,7 +581,8 @@ static void launch_stream_t(const GemmParams &p, int nwg, hipStream_t s) {
   }
   GemmParams q = p;
   q.stream_slots = stream_slots((p.N + TILE_N - 1) / TILE_N, (p.KS + 3) / 4, nwg);
-  hipLaunchKernelGGL(kern, dim3(nwg), dim3(SNT), gemv_stream_lds_bytes(MR, p.KS, q.stream_slots), s, q);
+  hipLaunchKernelGGL(kern, dim3(nwg), dim3(SNT), gemv_stream_lds_bytes(MR, p.KS, q.stream_slots, SX == SX_GLOBAL), s,
+                     q);
 }
 
 template <int DT, int SDT, int MR, int SX>
@@ -530,29 +593,33 @@ static void launch_stream_pf(const GemmParams &p, int nwg, hipStream_t s) {
 }
 
 template <int DT, int SDT, int MR>
-static void launch_stream_x(const GemmParams &p, int nwg, hipStream_t s) {
+static void launch_stream_x(const GemmParams &p, int nwg, bool global_rows, hipStream_t s) {
+  if constexpr (MR > 2) {
+    if (global_rows) return launch_stream_pf<DT, SDT, MR, SX_GLOBAL>(p, nwg, s);
+  }
   if (p.kinv) launch_stream_pf<DT, SDT, MR, SX_SCATTER>(p, nwg, s);
   else if (p.kmap) launch_stream_pf<DT, SDT, MR, SX_GATHER>(p, nwg, s);
   else launch_stream_pf<DT, SDT, MR, SX_CONTIG>(p, nwg, s);
 }
 
 template <int DT, int SDT>
-static void launch_stream_m(const GemmParams &p, int nwg, hipStream_t s) {
+static void launch_stream_m(const GemmParams &p, int nwg, bool g, hipStream_t s) {
   switch (stream_rows(p.M)) {
-    case 1: launch_stream_x<DT, SDT, 1>(p, nwg, s); break;
-    case 2: launch_stream_x<DT, SDT, 2>(p, nwg, s); break;
-    case 4: launch_stream_x<DT, SDT, 4>(p, nwg, s); break;
-    case 8: launch_stream_x<DT, SDT, 8>(p, nwg, s); break;
-    default: launch_stream_x<DT, SDT, 16>(p, nwg, s); break;
+    case 1: launch_stream_x<DT, SDT, 1>(p, nwg, g, s); break;
+    case 2: launch_stream_x<DT, SDT, 2>(p, nwg, g, s); break;
+    case 4: launch_stream_x<DT, SDT, 4>(p, nwg, g, s); break;
+    case 8: launch_stream_x<DT, SDT, 8>(p, nwg, g, s); break;
+    default: launch_stream_x<DT, SDT, 16>(p, nwg, g, s); break;
   }
 }
 
-void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s) {
+void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, bool global_rows,
+                             hipStream_t s) {
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf && sbf) launch_stream_m<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, nwg, s);
-  else if (bf) launch_stream_m<OC_DTYPE_BF16, OC_DTYPE_F16>(p, nwg, s);
-  else if (sbf) launch_stream_m<OC_DTYPE_F16, OC_DTYPE_BF16>(p, nwg, s);
-  else launch_stream_m<OC_DTYPE_F16, OC_DTYPE_F16>(p, nwg, s);
+  if (bf && sbf) launch_stream_m<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, nwg, global_rows, s);
+  else if (bf) launch_stream_m<OC_DTYPE_BF16, OC_DTYPE_F16>(p, nwg, global_rows, s);
+  else if (sbf) launch_stream_m<OC_DTYPE_F16, OC_DTYPE_BF16>(p, nwg, global_rows, s);
+  else launch_stream_m<OC_DTYPE_F16, OC_DTYPE_F16>(p, nwg, global_rows, s);
 }
 
 }  // namespace oc

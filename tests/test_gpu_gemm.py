@@ -41,13 +41,15 @@ def _oracle_out(layer, x: torch.Tensor, dtype="bf16", bias=None):
 
 @pytest.fixture
 def decode_kernel(monkeypatch):
-    """use(kind) selects the decode (M <= 2) kernel: "stream" (balanced weight
-    range per workgroup, the default), "tile" (one 16-column tile per
-    workgroup) or "split" (K-split work items)."""
+    """use(kind) selects the small-batch kernel: "stream" (balanced weight
+    range per workgroup, the default), "global" (the same ranges, 3..16 rows
+    read from global memory instead of staged), "tile" (one 16-column tile
+    per workgroup) or "split" (K-split work items, M <= 2)."""
     from onecomp_runtime import _hip
 
     def use(kind: str) -> None:
-        monkeypatch.setenv("ONECOMP_HIP_GEMV_STREAM", "1" if kind == "stream" else "0")
+        monkeypatch.setenv("ONECOMP_HIP_GEMV_STREAM", "1" if kind in ("stream", "global") else "0")
+        monkeypatch.setenv("ONECOMP_HIP_STREAM_GLOBAL", "1" if kind == "global" else "0")
         monkeypatch.setenv("ONECOMP_HIP_GEMV_SPLIT", "1" if kind == "split" else "0")
         _hip.gemm_workspace_bytes.cache_clear()  # workspace sizes follow the kernel
 
@@ -772,3 +774,63 @@ def _gemm_bias_auto(mod, x, bias):
     from onecomp_runtime import kernels
 
     return kernels.int4_gemm(x, mod.tiled(), in_features=mod.in_features, kmap=mod.kmap, kinv=mod.kinv, bias=bias)
+
+
+# -- stream kernel over activation rows in global memory (3 <= M <= 16, rows
+# beyond LDS, a tile count that whole tiles would spread unevenly): exact
+# dequantization, MFMAs accumulated across K steps, no staging. ---------------
+@pytest.mark.parametrize("M,K,N,kind", [
+    (4, 17408, 5120, "plain"),
+    (8, 17408, 5120, "actorder"),   # decode M=8 layer (rows gathered first)
+    (16, 5120, 17408, "actorder"),
+    (16, 8224, 4112, "plain"),      # 257 K steps (units past the tile's end), a ragged tile
+    (12, 16384, 4112, "gs128"),
+    (3, 20000, 5120, "kmap"),       # act-order without kinv
+])
+def test_stream_global_rows_matches_oracle(M, K, N, kind, decode_kernel):
+    from onecomp_runtime import kernels, synthetic
+
+    decode_kernel("global")
+    kw = dict(seed=140 + K % 97 + N % 89 + M)
+    if kind in ("actorder", "kmap"):
+        kw["act_order"] = True
+    if kind == "gs128":
+        kw["groupsize"] = 128
+    layer = synthetic.gptq_layer(K, N, **kw)
+    mod = _module_for(layer)
+    if mod.kmap is None:
+        assert _uses_stream(mod, M)  # the counter area alone: the stream kernel, no gathered rows
+    x = synthetic.activations(M, K, seed=141)
+    say(f"stream global rows K={K} N={N} kind={kind} M={M}")
+    kinv = None if kind == "kmap" else mod.kinv
+    out = kernels.int4_gemm(x.to(DEV), mod.tiled(), in_features=K, kmap=mod.kmap, kinv=kinv)
+    assert_gemm_close(out, _oracle_out(layer, x), f"stream global K={K} N={N} {kind} M={M}")
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_stream_global_rows_one_hot_bit_exact(M, decode_kernel):
+    from onecomp_runtime import synthetic
+
+    decode_kernel("global")
+    K, N = 4096, 4112
+    layer = synthetic.gptq_layer(K, N, seed=142)
+    mod = _module_for(layer)
+    assert _uses_stream(mod, M)
+    qw, sc, qz, g_idx = layer_oracle_inputs(layer)
+    wd = O.dequant_gptq(qw, sc, qz, g_idx, K, N, "bf16", layer.v1)
+    rng = np.random.default_rng(7)
+    for rep in range(2):
+        ks = rng.choice(K, M, replace=False)
+        x = torch.zeros((M, K), dtype=torch.bfloat16)
+        x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+        say(f"stream global one-hot M={M} rep={rep}")
+        out = _gemm_raw(mod, x.to(DEV), AUTO)
+        assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, torch.bfloat16))
+    # deterministic across calls and equal to the whole-tile kernel within tolerance
+    x = synthetic.activations(M, K, seed=143).to(DEV)
+    a = _gemm_raw(mod, x, AUTO)
+    assert torch.equal(_gemm_raw(mod, x, AUTO), a)
+    decode_kernel("tile")
+    assert not _uses_stream(mod, M)
+    b = _gemm_raw(mod, x, AUTO)
+    assert (a.float() - b.float()).abs().max().item() <= 2e-2 * a.float().abs().max().item()
