@@ -188,10 +188,15 @@ def test_planner_takes_stream_mfma_for_small_batches():
     cases = {
         (8, 5120, 5120, 1): True, (8, 5120, 17408, 1): True, (8, 5120, 1024, 1): True,
         (4, 5120, 17408, 0): True, (16, 2048, 16384, 0): True,
-        (8, 17408, 5120, 1): False,   # 8 rows of K = 17408 exceed LDS
+        (8, 17408, 5120, 1): False,   # 8 rows of K = 17408 exceed LDS: global rows (below)
         (16, 4096, 4096, 0): False,   # 128 KB staged for 32 KB of weights per workgroup
         (17, 1024, 16384, 0): False,  # beyond 16 rows
     }
     for (M, K, N, kmap), stream in cases.items():
         nbytes = f(M, N, K, 32, kmap, 0)
         assert (nbytes == cells) == stream, (M, K, N, kmap, nbytes)
+    # Rows beyond LDS on an uneven tile count: the same ranges over rows read
+    # from global memory (the counter area, plus act-order rows gathered first).
+    assert f(4, 5120, 17408, 32, 0, 0) == cells
+    assert f(8, 5120, 17408, 32, 1, 0) == cells + 8 * 17408 * 2
+    assert f(16, 4096, 4096, 32, 0, 0) == 0  # 256 tiles: whole tiles are even
