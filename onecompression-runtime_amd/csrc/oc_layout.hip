@@ -161,10 +161,14 @@ __global__ __launch_bounds__(1024) void scatter_rows_kernel(const uint16_t *__re
 }
 }  // namespace
 
+constexpr int SCATTER_MIN_ROWS = 32;  // rows from which one workgroup per row pays
+
 void launch_gather_cols(const void *a, int64_t lda, int M, int K_logical, const int32_t *kmap,
                         const uint16_t *kinv, int K_phys, void *out, void *stream) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (kinv && K_phys <= SCATTER_ROW_MAX) {
+  // One workgroup per row pays for many rows; a few rows (M = 8: 8 workgroups)
+  // spread better as one thread per physical element.
+  if (kinv && K_phys <= SCATTER_ROW_MAX && M >= SCATTER_MIN_ROWS) {
     hipLaunchKernelGGL(scatter_rows_kernel, dim3(M), dim3(1024), 0, s, static_cast<const uint16_t *>(a), lda,
                        K_logical, kinv, K_phys, static_cast<uint16_t *>(out));
     return;
