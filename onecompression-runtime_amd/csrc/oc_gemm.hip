@@ -1123,16 +1123,20 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
         env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
       // ONECOMP_HIP_STREAM_GLOBAL=1 (read per call; tests) skips the staged form.
       const bool global_only = env_int("ONECOMP_HIP_STREAM_GLOBAL", 0) != 0;
-      sp.stream_wgs = global_only ? 0 : gemv_stream_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
-      if (sp.stream_wgs > 0) {
-        sp.gather = false;
-        return sp;
-      }
-      // Rows beyond LDS: the same ranges over gathered rows in global memory.
-      sp.stream_wgs = gemv_stream_global_wgs(M, N, ksteps, device_cus(), COUNTER_BYTES);
-      if (sp.stream_wgs > 0) {
+      const int cus = device_cus();
+      const int staged = global_only ? 0 : gemv_stream_wgs(M, N, ksteps, cus, COUNTER_BYTES);
+      // Rows beyond LDS, or a narrow layer the staged form would run on under
+      // half the CUs: the same ranges over rows read from global memory.
+      const int global = staged >= cus / 2 ? 0 : gemv_stream_global_wgs(M, N, ksteps, cus, COUNTER_BYTES);
+      if (global > staged) {
+        sp.stream_wgs = global;
         sp.stream_global = true;
         return sp;  // sp.gather as planned: act-order rows are gathered first
+      }
+      if (staged > 0) {
+        sp.stream_wgs = staged;
+        sp.gather = false;
+        return sp;
       }
     }
     sp.mt = std::max(1, (M + 15) / 16);

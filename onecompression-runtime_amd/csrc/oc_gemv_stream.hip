@@ -503,9 +503,10 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
       if (out_ok) store_c<DT>(p.c, static_cast<int64_t>(m) * p.ldc + n, v + bias_at(p, n));
       continue;
     }
-    // A cut tile: the range's first (this workgroup is its upper contributor)
-    // or its last (the lower one). Its cell: [lower workgroup][m][column].
-    const bool upper = slot == 0;
+    // A cut tile has two contributors: this workgroup is the upper one when
+    // the tile starts before its range, else the lower. Its cell: [lower
+    // workgroup][m][column].
+    const bool upper = t * QT < u0;
     const int lower_b = upper ? b - 1 : b;
     unsigned long long *cell = reinterpret_cast<unsigned long long *>(p.counters) + (lower_b * MR + m) * 16 + cc;
     const unsigned long long mine = (1ull << 32) | __float_as_uint(v);
@@ -554,11 +555,16 @@ int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
 int gemv_stream_global_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
   if (M < 3 || M > 16) return 0;
   const int MR = stream_rows(M);
-  const int64_t tiles = (N + TILE_N - 1) / TILE_N, QT = (KS + 3) / 4, nwg = cus;
-  // Worth it where whole tiles would load compute units unevenly (a tile
-  // count that is not a multiple of the workgroups), with the range
-  // conditions of the staged form.
-  if (tiles < nwg || tiles % nwg == 0) return 0;
+  const int64_t tiles = (N + TILE_N - 1) / TILE_N, QT = (KS + 3) / 4;
+  int64_t nwg = cus;
+  if (tiles < cus) {
+    // Narrow layers: two workgroups per tile, each exactly half of it (an
+    // even unit count per tile keeps every tile at two contributors).
+    if (2 * tiles > cus || QT % 2 != 0) return 0;
+    nwg = 2 * tiles;
+  } else if (tiles % nwg == 0) {
+    return 0;  // whole tiles already load compute units evenly
+  }
   const int64_t q1 = tiles * QT / nwg + 1;
   if ((q1 + QT - 1) / QT + 1 > SNTL) return 0;
   const int nslots = stream_slots(tiles, static_cast<int>(QT), static_cast<int>(nwg));

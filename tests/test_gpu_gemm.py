@@ -675,7 +675,7 @@ def _uses_stream(mod, M):
     (3, 160, 4104, "actorder"),     # 5 K steps, cut tiles, a ragged tile
     (5, 96, 4096, "plain"),         # 3 K steps: lanes past the tile's end
     (12, 1040, 16392, "gs26"),      # padded groups, a ragged tile
-    (8, 5120, 1024, "actorder"),    # 64 tiles: one workgroup per tile
+    (4, 4096, 3200, "plain"),       # 200 tiles: one workgroup per tile
     (4, 128, 20000, "kmap"),        # gathered through kmap (no kinv)
     (16, 2048, 8192, "gs128"),
     (9, 64, 24576, "plain"),        # 6 tiles per workgroup
@@ -786,6 +786,8 @@ def _gemm_bias_auto(mod, x, bias):
     (16, 8224, 4112, "plain"),      # 257 K steps (units past the tile's end), a ragged tile
     (12, 16384, 4112, "gs128"),
     (3, 20000, 5120, "kmap"),       # act-order without kinv
+    (8, 5120, 1024, "actorder"),    # 64 tiles: two workgroups per tile (half-tile ranges)
+    (5, 4096, 2000, "plain"),       # 125 tiles, a ragged last tile, half-tile ranges
 ])
 def test_stream_global_rows_matches_oracle(M, K, N, kind, decode_kernel):
     from onecomp_runtime import kernels, synthetic

@@ -186,7 +186,7 @@ def test_planner_takes_stream_mfma_for_small_batches():
     cells = 512 * 1024
     # (M, K_phys, N, has_kmap) -> stream?
     cases = {
-        (8, 5120, 5120, 1): True, (8, 5120, 17408, 1): True, (8, 5120, 1024, 1): True,
+        (8, 5120, 5120, 1): True, (8, 5120, 17408, 1): True,
         (4, 5120, 17408, 0): True, (16, 2048, 16384, 0): True,
         (8, 17408, 5120, 1): False,   # 8 rows of K = 17408 exceed LDS: global rows (below)
         (16, 4096, 4096, 0): False,   # 128 KB staged for 32 KB of weights per workgroup
@@ -200,3 +200,5 @@ def test_planner_takes_stream_mfma_for_small_batches():
     assert f(4, 5120, 17408, 32, 0, 0) == cells
     assert f(8, 5120, 17408, 32, 1, 0) == cells + 8 * 17408 * 2
     assert f(16, 4096, 4096, 32, 0, 0) == 0  # 256 tiles: whole tiles are even
+    # A narrow layer (64 tiles) runs two workgroups per tile over global rows.
+    assert f(8, 1024, 5120, 32, 1, 0) == cells + 8 * 5120 * 2
