@@ -904,10 +904,13 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const int64_t 
   for (int i = tid; i < (ROUTE_WAVES + 1) * E; i += ROUTE_THREADS) cnt[i] = 0;
   __syncthreads();
 
+  // Expert of pair q (E: dropped or past the wave's pairs).
+  auto expert_of = [&](int q) {
+    const int64_t id = q < q_end ? ids[q] : -1;
+    return id >= 0 && id < E ? static_cast<int>(id) : E;
+  };
   // Same-expert lanes of a batch, this lane's rank among them and their count.
-  auto match = [&](int q, int &e, int &rank, int &count) {
-    int64_t id = q < q_end ? ids[q] : -1;
-    e = id >= 0 && id < E ? static_cast<int>(id) : E;
+  auto match = [&](int e, int &rank, int &count) {
     uint64_t mask = __ballot(1);
     for (int b = 0; b < bits; ++b) {
       const uint64_t bb = __ballot((e >> b) & 1);
@@ -917,10 +920,19 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const int64_t 
     count = __popcll(mask);
   };
   int32_t *wc = cnt + w * E;
-  for (int q0 = q_begin; q0 < q_end; q0 += 64) {
-    int e, rank, count;
-    match(q0 + lane, e, rank, count);
-    if (e < E && rank == count - 1) wc[e] += count;
+  // Rounds of RB batches: their id loads go out together.
+  constexpr int RB = 8;
+  for (int q0 = q_begin; q0 < q_end; q0 += 64 * RB) {
+    int ex[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) ex[r] = expert_of(q0 + 64 * r + lane);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (q0 + 64 * r >= q_end) break;
+      int rank, count;
+      match(ex[r], rank, count);
+      if (ex[r] < E && rank == count - 1) wc[ex[r]] += count;
+    }
   }
   __syncthreads();
 
@@ -957,14 +969,22 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const int64_t 
   }
   __syncthreads();
 
-  for (int q0 = q_begin; q0 < q_end; q0 += 64) {
-    int e, rank, count;
-    match(q0 + lane, e, rank, count);
-    // Every lane reads its base before the group's last lane advances it
-    // (one wave's LDS accesses complete in program order).
-    const int base = e < E ? wc[e] : 0;
-    if (e < E) sorted[base + rank] = q0 + lane;
-    if (e < E && rank == count - 1) wc[e] = base + count;
+  for (int q0 = q_begin; q0 < q_end; q0 += 64 * RB) {
+    int ex[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) ex[r] = expert_of(q0 + 64 * r + lane);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      if (q0 + 64 * r >= q_end) break;
+      const int e = ex[r];
+      int rank, count;
+      match(e, rank, count);
+      // Every lane reads its base before the group's last lane advances it
+      // (one wave's LDS accesses complete in program order).
+      const int base = e < E ? wc[e] : 0;
+      if (e < E) sorted[base + rank] = q0 + 64 * r + lane;
+      if (e < E && rank == count - 1) wc[e] = base + count;
+    }
   }
 }
 
