@@ -179,7 +179,7 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  * with a 512 KB counter area (small-batch calls, M <= 16: arrival counters
  * and the 64-bit cells through which two workgroups sharing an output tile
  * exchange their partial sums), then holds gathered activations (kmap with
- * M > 2, when the whole-tile kernel serves the batch) and fp32
+ * M > 2, unless the batch's rows are staged in LDS) and fp32
  * split-K partials (large M with few output tiles, or a decode call whose K
  * is split over workgroups). The counter area must hold zeros the
  * first time a workspace is used (e.g. allocate it zero-filled) and every
