@@ -1139,7 +1139,11 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     // kernel's MFMA form when their activation rows fit in LDS (it stages
     // act-order rows itself: no gather pass). ONECOMP_HIP_GEMV_STREAM=0
     // (read per call) keeps them on the whole-tile MFMA kernel below.
-    if (automatic && M >= 3 && M <= 16 && ilog2_exact(group_rows / 32) >= 0 &&
+    // Not for layers the whole-tile kernel already spreads evenly and reads
+    // without a gather (measured M = 8 K=N=4096: 6.7 us whole tiles, 7.7 us
+    // staged; M = 16: 7.7 vs 9.3 us).
+    const bool even_plain = !has_kmap && ((N + TILE_N - 1) / TILE_N) % device_cus() == 0;
+    if (automatic && M >= 3 && M <= 16 && !even_plain && ilog2_exact(group_rows / 32) >= 0 &&
         env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
       // ONECOMP_HIP_STREAM_GLOBAL=1 (read per call; tests) skips the staged form.
       const bool global_only = env_int("ONECOMP_HIP_STREAM_GLOBAL", 0) != 0;

@@ -669,16 +669,16 @@ def _uses_stream(mod, M):
 
 
 @pytest.mark.parametrize("M,K,N,kind", [
-    (16, 2048, 16384, "plain"),     # 4 tiles per workgroup
+    (16, 2048, 16400, "plain"),     # 4 tiles per workgroup and a ragged one
     (8, 5120, 5120, "actorder"),    # decode M=8 layers
     (8, 5120, 17408, "actorder"),
     (3, 160, 4104, "actorder"),     # 5 K steps, cut tiles, a ragged tile
-    (5, 96, 4096, "plain"),         # 3 K steps: lanes past the tile's end
+    (5, 96, 4112, "plain"),         # 3 K steps: lanes past the tile's end
     (12, 1040, 16392, "gs26"),      # padded groups, a ragged tile
     (4, 4096, 3200, "plain"),       # 200 tiles: one workgroup per tile
     (4, 128, 20000, "kmap"),        # gathered through kmap (no kinv)
-    (16, 2048, 8192, "gs128"),
-    (9, 64, 24576, "plain"),        # 6 tiles per workgroup
+    (16, 2048, 8208, "gs128"),
+    (9, 64, 24592, "plain"),        # 6 tiles per workgroup
 ])
 def test_stream_mfma_matches_oracle(M, K, N, kind, decode_kernel):
     from onecomp_runtime import kernels, synthetic
@@ -708,7 +708,7 @@ def test_stream_mfma_one_hot_bit_exact(kind, M, decode_kernel):
     from onecomp_runtime import synthetic
 
     decode_kernel("stream")
-    K, N = 1024, 16384
+    K, N = 1024, 16400
     kw = dict(seed=132)
     dtype = torch.float16 if kind == "fp16" else torch.bfloat16
     if kind == "v2":

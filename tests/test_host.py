@@ -187,7 +187,8 @@ def test_planner_takes_stream_mfma_for_small_batches():
     # (M, K_phys, N, has_kmap) -> stream?
     cases = {
         (8, 5120, 5120, 1): True, (8, 5120, 17408, 1): True,
-        (4, 5120, 17408, 0): True, (16, 2048, 16384, 0): True,
+        (4, 5120, 17408, 0): True, (16, 2048, 16400, 0): True,
+        (16, 2048, 16384, 0): False,  # 1024 tiles, no gather: whole tiles are even
         (8, 17408, 5120, 1): False,   # 8 rows of K = 17408 exceed LDS: global rows (below)
         (16, 4096, 4096, 0): False,   # 128 KB staged for 32 KB of weights per workgroup
         (17, 1024, 16384, 0): False,  # beyond 16 rows
