@@ -361,24 +361,23 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemmParams p) {
     });
   }
 
-  // acc[tt][i] = row 16tt + 4*quad + i, column c16. Fixed LDS tree over the NW waves.
-  __shared__ float red[NW / 2][MT * 16][TILE_N + 1];
+  // acc[tt][i] = row 16tt + 4*quad + i, column c16. Waves 1.. park their sums
+  // in LDS behind one barrier; wave 0 adds them in wave order.
+  __shared__ float red[NW - 1][MT * 16][TILE_N + 1];
+  if (wave > 0) {
 #pragma unroll
-  for (int half = NW / 2; half >= 1; half >>= 1) {
-    if (wave >= half && wave < 2 * half) {
+    for (int tt = 0; tt < MT; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[wave - 1][16 * tt + 4 * quad + i][c16] = acc[tt][i];
+  }
+  __syncthreads();
+  if (wave == 0) {
+#pragma unroll
+    for (int w = 0; w < NW - 1; ++w)
 #pragma unroll
       for (int tt = 0; tt < MT; ++tt)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) red[wave - half][16 * tt + 4 * quad + i][c16] = acc[tt][i];
-    }
-    __syncthreads();
-    if (wave < half) {
-#pragma unroll
-      for (int tt = 0; tt < MT; ++tt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[tt][i] += red[wave][16 * tt + 4 * quad + i][c16];
-    }
-    __syncthreads();
+        for (int i = 0; i < 4; ++i) acc[tt][i] += red[w][16 * tt + 4 * quad + i][c16];
   }
   if (wave != 0 || n >= p.N) return;
   const float bv = bias_at(p, n);
