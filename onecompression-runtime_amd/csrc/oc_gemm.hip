@@ -118,10 +118,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
       for (int base = 0; base < per_row; base += NT * SB) {
         uint4 raw[SB];
 #pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int i = base + NT * u + tid;
-          raw[u] = i < per_row ? arow[i] : make_uint4(0, 0, 0, 0);
-        }
+        for (int u = 0; u < SB; ++u)  // clamped, not guarded: a branch around a load waits for it
+          raw[u] = arow[min(base + NT * u + tid, per_row - 1)];
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
           const int i = base + NT * u + tid;
@@ -153,12 +151,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
       for (int base = 0; base < octets; base += NT * SB) {
         uint4 xv[SB], rv[SB];
 #pragma unroll
-        for (int u = 0; u < SB; ++u) {
-          const int i = base + NT * u + tid;
-          if (i < octets) {
-            xv[u] = reinterpret_cast<const uint4 *>(arow)[i];
-            rv[u] = kinv4[i];
-          }
+        for (int u = 0; u < SB; ++u) {  // clamped loads (the stores below are guarded)
+          const int i = min(base + NT * u + tid, octets - 1);
+          xv[u] = reinterpret_cast<const uint4 *>(arow)[i];
+          rv[u] = kinv4[i];
         }
 #pragma unroll
         for (int u = 0; u < SB; ++u) {
@@ -203,13 +199,17 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 #pragma unroll
   for (int m = 0; m < MR; ++m) acc[m] = 0.f;
   const uint32_t magic = MAGIC;
-  for (int base = lp; base < ks_end; base += NPH * DOT_PF) {
+  // This lane's K steps lp, lp + NPH, ..., padded to whole rounds of DOT_PF
+  // (the padding re-reads the last step and adds nothing); each stage is
+  // consumed and then refilled in place.
+  const int nks = lp < ks_end ? (ks_end - lp + NPH - 1) / NPH : 0;
+  const int nks_pad = (nks + DOT_PF - 1) / DOT_PF * DOT_PF;
+  for (int i0 = 0; i0 < nks_pad; i0 += DOT_PF) {
 #pragma unroll
     for (int f = 0; f < DOT_PF; ++f) {
-      const int ks = base + NPH * f;
-      if (ks >= ks_end) break;
-      const Stage cur = st[f];
-      load(st[f], min(ks + NPH * DOT_PF, ks_last));
+      const bool valid = i0 + f < nks;
+      const int ks = min(lp + NPH * (i0 + f), ks_last);
+      Stage &cur = st[f];
       // Two partial sums per row (words 0-1 and 2-3) shorten the dot2 chain.
       float d[MR][2];
 #pragma unroll
@@ -237,8 +237,10 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
 #pragma unroll
       for (int m = 0; m < MR; ++m) {
         const float2 xs = xsum[m * KSP + ks];
-        acc[m] = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, (d[m][0] + d[m][1]) - xs.y), acc[m]);
+        const float v = __builtin_fmaf(s, __builtin_fmaf(-zf, xs.x, (d[m][0] + d[m][1]) - xs.y), acc[m]);
+        acc[m] = valid ? v : acc[m];
       }
+      load(cur, min(lp + NPH * (i0 + f + DOT_PF), ks_last));
     }
   }
 
