@@ -2,8 +2,8 @@
 
 A numpy restatement of the reference's CPU ("eager"/"packed") path. Only
 tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-it, and only as the checker (or the timed CPU baseline); the product never
-calls it.
+it, and only to check results against (or as the timed CPU baseline); the
+product never calls it.
 
 Values of 16-bit floats are carried as float32 arrays holding exactly
 representable values; rounding to a 16-bit type is explicit (``round_to``).
