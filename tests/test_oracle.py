@@ -1,5 +1,5 @@
-"""Pins the CPU oracle (oracle/onecomp_oracle.py) before it is trusted as
-the parity checker: known answers derived with exact rational arithmetic
+"""Pins the CPU oracle (oracle/onecomp_oracle.py) before parity tests trust
+it as their reference: known answers derived with exact rational arithmetic
 (tests/golden/kats.json), torch's own conversions and 16-bit arithmetic (the
 reference's arithmetic boundary), format invariants and float64 brute force.
 CPU only.
