@@ -415,17 +415,37 @@ __device__ __forceinline__ RtnParam rtn_param(const GemmParams &p, int g, int n)
   return r;
 }
 
-// Sum of the split-K partials in split order, plus bias, rounded once.
+// Sum of the split-K partials in split order, plus bias, rounded once. A
+// thread adds 4 adjacent outputs (N % 8 == 0 keeps them in one row); the
+// partials of up to 8 splits are loaded together before the in-order sum.
+constexpr int REDUCE_UNROLL = 8;
 template <int DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t MN = static_cast<int64_t>(p.M) * p.N;
+  const int64_t idx = 4 * (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x);
   if (idx >= MN) return;
   const int n = static_cast<int>(idx % p.N);
   const int row = static_cast<int>(idx / p.N);
-  float v = 0.f;
-  for (int s = 0; s < p.ksplit; ++s) v += p.partials[s * MN + idx];
-  store_c<DT>(p.c, static_cast<int64_t>(row) * p.ldc + n, v + bias_at(p, n));
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < p.ksplit; s0 += REDUCE_UNROLL) {
+    float4 t[REDUCE_UNROLL];
+#pragma unroll
+    for (int j = 0; j < REDUCE_UNROLL; ++j)  // clamped, not guarded: the loads go out together
+      t[j] = *reinterpret_cast<const float4 *>(p.partials + min(s0 + j, p.ksplit - 1) * MN + idx);
+#pragma unroll
+    for (int j = 0; j < REDUCE_UNROLL; ++j) {
+      if (s0 + j >= p.ksplit) break;
+      v.x += t[j].x;
+      v.y += t[j].y;
+      v.z += t[j].z;
+      v.w += t[j].w;
+    }
+  }
+  const int64_t o = static_cast<int64_t>(row) * p.ldc + n;
+  store_c<DT>(p.c, o, v.x + bias_at(p, n));
+  store_c<DT>(p.c, o + 1, v.y + bias_at(p, n + 1));
+  store_c<DT>(p.c, o + 2, v.z + bias_at(p, n + 2));
+  store_c<DT>(p.c, o + 3, v.w + bias_at(p, n + 3));
 }
 
 // ---------------------------------------------------------------------------
@@ -1302,7 +1322,7 @@ void launch_tiled_t(const GemmParams &p, hipStream_t s) {
     hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0,
                        s, p);
   }
 }
@@ -1339,7 +1359,7 @@ void launch_big(const GemmParams &p, hipStream_t s) {
   hipLaunchKernelGGL((gemm_big_kernel<DT, SDT, BIG_WM, BIG_WN, BIG_KPS, false>), grid, dim3(256), 0, s, p);
   if (p.ksplit > 1) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
-    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn + 255) / 256)), dim3(256), 0,
+    hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0,
                        s, p);
   }
 }
