@@ -322,6 +322,10 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * 8u : NOWHERE), 0, 0);
     pu += SW;
   };
+  // Activations are staged before the weight prefetch goes out: memory
+  // waits count in issue order, so staging after it would also wait for
+  // the prefetch.
+  if (one_batch && n_items > 0) stage_store(0);
   // The prologue issues each stage's loads in the loop's order (no
   // regrouping by the scheduler): the loop's wait counts assume it.
   Stage st[PF];
@@ -331,7 +335,6 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  if (one_batch && n_items > 0) stage_store(0);
   if constexpr (SX == SX_SCATTER) {
     // Step sums from the staged pairs.
     barrier_no_fence();
