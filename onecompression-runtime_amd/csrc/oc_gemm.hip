@@ -96,6 +96,8 @@ __global__ __launch_bounds__(64 * WAVES) void gemv_dot_kernel(GemmParams p) {
   };
   Stage st[DOT_PF];
   auto load = [&](Stage &S, int ks) {
+    // Default cache policy: non-temporal loads (CPOL_WEIGHT_STREAM) made
+    // this kernel slower (K=5120 N=1024 M=1: 4.3 -> 5.1 us).
     S.q = qt4[ks * TILE_N];
     const int g = ks >> p.gshift;
     S.s = stp[g * TILE_N];
@@ -318,10 +320,10 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemmParams p) {
     const int ks = 4 * qs + quad;
     const bool kin = ks < KS;
     const uint32_t g = static_cast<uint32_t>(group_of(p, kin ? ks : 0));
-    const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, kin ? q_base + 256u * ks : NOWHERE, 0, 0);
+    const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, kin ? q_base + 256u * ks : NOWHERE, 0,CPOL_WEIGHT_STREAM);
     S.q = make_uint4(q[0], q[1], q[2], q[3]);
-    S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, kin ? s_base + 32u * g : NOWHERE, 0, 0);
-    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, kin ? z_base + 8u * g : NOWHERE, 0, 0);
+    S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, kin ? s_base + 32u * g : NOWHERE, 0,CPOL_WEIGHT_STREAM);
+    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, kin ? z_base + 8u * g : NOWHERE, 0,CPOL_WEIGHT_STREAM);
 #pragma unroll
     for (int tt = 0; tt < MT; ++tt) {
       const uint32_t off = kin && a_row[tt] != NOWHERE ? a_row[tt] + 64u * ks : NOWHERE;

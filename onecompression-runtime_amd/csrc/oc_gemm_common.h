@@ -139,6 +139,13 @@ __device__ __forceinline__ float dot2acc(uint32_t b, uint32_t x, float acc) {
   }
 }
 
+// Cache policy of the weight, scale and zero loads of the stream and
+// whole-tile MFMA GEMV kernels (the aux operand of the buffer loads): nt,
+// non-temporal. Each of those bytes is read once per call. Measured on a
+// decode sweep of four layers: 5 % faster per step; a single layer replayed
+// back to back is ~4 % slower with it.
+constexpr int CPOL_WEIGHT_STREAM = 2;
+
 template <int DT>
 __device__ __forceinline__ float half_to_f32(uint32_t h16) {
   if constexpr (DT == OC_DTYPE_BF16) return bf16_to_f32(static_cast<uint16_t>(h16));

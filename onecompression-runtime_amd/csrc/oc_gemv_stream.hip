@@ -122,8 +122,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     else xsum[m * KS4 + ks] = make_float2(sum, dot_base<DT>() * sum);
   };
 
-  // ---- activation staging, batch by batch; the weight stream starts after
-  // the first batch's loads so both are in flight together ----
+  // ---- activation staging, batch by batch, before the weight stream ----
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
   const int n_items = GL ? 0 : SX == SX_SCATTER ? (p.K_logical >> 3) : KS * 4;  // octets to stage
   const uint4 *kinv4 = reinterpret_cast<const uint4 *>(p.kinv);
@@ -207,9 +206,10 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
       }
     }
   };
-  // One batch covers the rows (the common case): its loads go out first and
-  // the weight prefetch follows, so both are in flight together. Longer or
-  // ragged rows are staged before the weight stream starts.
+  // One batch covers the rows (the common case): its loads go out first, the
+  // LDS zeroing below runs while they are in flight, and they are stored
+  // before the weight prefetch is issued. Longer or ragged rows are staged
+  // batch by batch.
   const bool one_batch = n_items <= SNT * SB && (SX != SX_SCATTER || (p.K_logical & 7) == 0);
   if (one_batch && n_items > 0) stage_load(0);
 
@@ -297,9 +297,9 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     const bool in = pu < u1;
     const uint32_t qo = q_lane + (in ? qb : NOWHERE), so = s_lane + (in ? gb * 32u : NOWHERE);
     if constexpr (GL) {
-      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0, 0);
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0,CPOL_WEIGHT_STREAM);
       S.q = make_uint4(q[0], q[1], q[2], q[3]);
-      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0, 0);
+      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0,CPOL_WEIGHT_STREAM);
       const int ks = 4 * (pu % QT) + h;  // this lane's K step (steps past KS read zeros)
       const bool a_in = in && ks < KS && a_row != NOWHERE;
 #pragma unroll
@@ -311,15 +311,15 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     } else if constexpr (MF) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        S.q[j] = __builtin_amdgcn_raw_buffer_load_b32(q_rs, qo + 256u * j, 0, 0);
-        S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 32 * (j >> gs2), 0);
+        S.q[j] = __builtin_amdgcn_raw_buffer_load_b32(q_rs, qo + 256u * j, 0,CPOL_WEIGHT_STREAM);
+        S.s[j] = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 32 * (j >> gs2),CPOL_WEIGHT_STREAM);
       }
     } else {
-      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0, 0);
+      const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0,CPOL_WEIGHT_STREAM);
       S.q = make_uint4(q[0], q[1], q[2], q[3]);
-      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0, 0);
+      S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0,CPOL_WEIGHT_STREAM);
     }
-    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * 8u : NOWHERE), 0, 0);
+    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * 8u : NOWHERE), 0,CPOL_WEIGHT_STREAM);
     pu += SW;
   };
   // Activations are staged before the weight prefetch goes out: memory
