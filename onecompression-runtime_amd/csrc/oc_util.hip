@@ -153,7 +153,12 @@ __global__ __launch_bounds__(256) void rtn_embedding_vec_kernel(
   uint4 lo = make_uint4(0, 0, 0, 0), hi = make_uint4(0, 0, 0, 0);
   const int64_t id = resolve_id(ids, t, V, bad_flag);
   if (id >= 0) {
-    const uint2 bytes = *reinterpret_cast<const uint2 *>(q + id * row_bytes + 8 * ch);
+    // Table bytes and output rows are touched once per call: non-temporal
+    // (4096 tokens of D=1024 from V=32768: 5.3 -> 5.0 us with the stores so
+    // marked).
+    using u32x2 = __attribute__((ext_vector_type(2))) uint32_t;
+    const u32x2 bv = __builtin_nontemporal_load(reinterpret_cast<const u32x2 *>(q + id * row_bytes + 8 * ch));
+    const uint2 bytes = make_uint2(bv[0], bv[1]);
     const int g = (16 * ch) / (D / G);
     RtnParam p;
     p.zq = round_to<ODT>(load_any_f32(zeros, id * G + g, zero_dtype));
@@ -161,8 +166,9 @@ __global__ __launch_bounds__(256) void rtn_embedding_vec_kernel(
     lo = rtn_dequant8<ODT>(bytes.x, p);
     hi = rtn_dequant8<ODT>(bytes.y, p);
   }
-  out[2 * idx] = lo;
-  out[2 * idx + 1] = hi;
+  using u32x4 = __attribute__((ext_vector_type(4))) uint32_t;
+  __builtin_nontemporal_store(u32x4{lo.x, lo.y, lo.z, lo.w}, reinterpret_cast<u32x4 *>(out + 2 * idx));
+  __builtin_nontemporal_store(u32x4{hi.x, hi.y, hi.z, hi.w}, reinterpret_cast<u32x4 *>(out + 2 * idx + 1));
 }
 
 template <int ODT>
