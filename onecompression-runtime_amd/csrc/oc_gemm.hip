@@ -420,6 +420,8 @@ __device__ __forceinline__ RtnParam rtn_param(const GemmParams &p, int g, int n)
 // Sum of the split-K partials in split order, plus bias, rounded once. A
 // thread adds 4 adjacent outputs (N % 8 == 0 keeps them in one row); the
 // partials of up to 8 splits are loaded together before the in-order sum.
+// Partials are written once and read once, both non-temporally (padded
+// gs26 M=256 K=1040 N=3072: 19.6 -> 18.7 us).
 constexpr int REDUCE_UNROLL = 8;
 template <int DT>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
@@ -432,8 +434,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
   for (int s0 = 0; s0 < p.ksplit; s0 += REDUCE_UNROLL) {
     float4 t[REDUCE_UNROLL];
 #pragma unroll
-    for (int j = 0; j < REDUCE_UNROLL; ++j)  // clamped, not guarded: the loads go out together
-      t[j] = *reinterpret_cast<const float4 *>(p.partials + min(s0 + j, p.ksplit - 1) * MN + idx);
+    for (int j = 0; j < REDUCE_UNROLL; ++j) {  // clamped, not guarded: the loads go out together
+      using f32x4 = __attribute__((ext_vector_type(4))) float;
+      const f32x4 v = __builtin_nontemporal_load(
+          reinterpret_cast<const f32x4 *>(p.partials + min(s0 + j, p.ksplit - 1) * MN + idx));
+      t[j] = make_float4(v[0], v[1], v[2], v[3]);
+    }
 #pragma unroll
     for (int j = 0; j < REDUCE_UNROLL; ++j) {
       if (s0 + j >= p.ksplit) break;
@@ -613,7 +619,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = m0 + 16 * t + 4 * quad + i;
-          if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
+          if (r < p.M) __builtin_nontemporal_store(acc[t][j][i], part + static_cast<int64_t>(r) * p.N + n);
         }
     }
   }
@@ -881,7 +887,7 @@ __global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void g
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = m0 + 16 * t + 4 * quad + i;
-            if (r < p.M) part[static_cast<int64_t>(r) * p.N + n] = acc[t][j][i];
+            if (r < p.M) __builtin_nontemporal_store(acc[t][j][i], part + static_cast<int64_t>(r) * p.N + n);
           }
       }
     }
