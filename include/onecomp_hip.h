@@ -116,6 +116,29 @@ int oc_int4_prepare(const int32_t *qweight, int32_t K, int32_t N,
                     void *st, int32_t *zt, void *stream);
 
 /*
+ * Device, checkpoint export (state_dict): the inverse of oc_int4_prepare.
+ * Writes the layer back in the checkpoint formats of the header comment, in
+ * the buffer layout the reference's modules register:
+ *   qweight int32 [ceil(out_rows/8), N]: code row k = physical row
+ *           row_src[k] (NULL: k itself); -1 or a row past K_phys is a zero code
+ *   scales  16-bit [out_groups, N] (st's dtype), qzeros int32 [out_groups, N/8];
+ *           groups past K_phys/group_rows get zero scales and zero words
+ *   zero_mode OC_ZERO_V1 stores zero - 1 (mod 16), OC_ZERO_V2 the zero.
+ * The reference layouts this reproduces: FusedInt4Linear's K padded to a
+ * multiple of 256 with zero rows/scales/zeros (layers/fused_int4_linear.py:
+ * 989-1005, :1016-1045; identity rows, out_rows = padded K);
+ * FusedInt4LinearPaddedGroups' 32-row group slots (:800-803, the physical
+ * order itself); PackedGPTQLinear's and FusedInt4LinearAnyGroup's verbatim
+ * checkpoint tensors (packed_gptq_linear.py:57-59, fused_int4_linear.py:
+ * 660-662; row_src = the physical row of each input row).
+ */
+int oc_int4_export(const int32_t *qt, const void *st, const int32_t *zt,
+                   int32_t N, int32_t K_phys, int32_t group_rows,
+                   const int32_t *row_src, int32_t out_rows,
+                   int32_t out_groups, int32_t zero_mode, int32_t *qweight,
+                   void *scales, int32_t *qzeros, void *stream);
+
+/*
  * Device, test/inspection and the fp32-activation path: dense out[N, K_logical]
  * (original K order) from the tiled layout, each value RNE_out(s * (code - zero))
  * exactly as quant_utils.dequant_gptq_to_fp (quant_utils.py:50-69).
@@ -155,9 +178,12 @@ int oc_int4_dequant(const int32_t *qweight, const void *scales,
  *   A'[m, k'] = kmap ? (kmap[k'] >= 0 ? A[m, kmap[k']] : 0) : A[m, k'],
  *   Wd[k', n] = RNE_a( f32(scale) * (code(k', n) - zero) )   (see oc_int4_prepare)
  * computed with fp32 accumulation and rounded once to a_dtype on store
- * (bias added in fp32). The decode regime (M <= 2) evaluates the same sum
- * with the scale and zero factored out of each 32-row group (exact for a
- * one-hot row; otherwise equal up to fp32 summation order). Replaces the
+ * (bias added in fp32). The small-batch kernels (M <= 16 on the balanced
+ * ranges, the whole-tile decode kernel) evaluate the same sum with the
+ * scale and zero factored out of each 32-row group: there each weight enters
+ * as the exact fp32 product s * (code - zero), not rounded to a_dtype first,
+ * so results differ from dequantize-then-multiply by at most that rounding
+ * per weight (and are identical for a one-hot row without bias). Replaces the
  * Triton launches of layers/fused_int4_linear.py:1194-1208
  * (FusedInt4Linear.forward), :504-532 (fused_int4_gemm) and :904-919
  * (FusedInt4LinearPaddedGroups.forward), and the act-order packed path

@@ -402,7 +402,9 @@ __device__ __forceinline__ uint32_t load_word(const GemmParams &p, const void *q
   if constexpr (FMT == FMT_GPTQ) {
     return static_cast<const uint32_t *>(qw)[((static_cast<int64_t>(tile) * p.KS + ks) * TILE_N + c16) * 4 + quad];
   } else {
-    const int n = TILE_N * tile + c16;
+    // Clamped like the RTN scale/zero rows: with N % 16 == 8 the upper lanes
+    // of the last tile name rows past the weight (their results are unused).
+    const int n = min(TILE_N * tile + c16, p.N - 1);
     return *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(qw) +
                                                static_cast<int64_t>(n) * p.row_bytes + 16 * ks + 4 * quad);
   }
@@ -1057,11 +1059,7 @@ struct Plan {
   bool stream_global;  // ... reading gathered activation rows from global memory
 };
 
-// Workspace layout, every regime: [counter area][gathered activations][fp32
-// partials]. The counter area holds the decode kernels' arrival counters and
-// swap cells; it must be zero when a workspace is first used and every call
-// leaves it zero, so no regime writes anything else there.
-constexpr size_t COUNTER_BYTES = 512 * 1024;
+// Workspace layout: see COUNTER_BYTES (oc_internal.h).
 constexpr int COUNTER_SLOTS = static_cast<int>(COUNTER_BYTES / sizeof(int));
 
 // Compute units of the current device (cached per device).
@@ -1395,12 +1393,16 @@ size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_
   return std::max(with_kinv, workspace_bytes(plan_gemm(M, N, K_phys, group_rows, true, regime, false), M, N, K_phys));
 }
 
-int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
-                 const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
-                 int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
-                 int32_t bias_dtype, void *c, int64_t ldc, void *workspace, size_t workspace_bytes_given,
-                 int32_t regime, void *stream) {
-  clear_error();
+}  // extern "C"
+
+namespace oc {
+
+int gemm_impl(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
+              const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
+              int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
+              int32_t bias_dtype, void *c, int64_t ldc, WorkspaceArg ws, int32_t regime, void *stream) {
+  void *workspace = ws.ptr;
+  const size_t workspace_bytes_given = ws.bytes;
   if (M < 0 || N <= 0 || K_phys <= 0 || K_logical <= 0)
     return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K_logical=%d K_phys=%d", M, N, K_logical, K_phys);
   if (M == 0) return OC_OK;
@@ -1432,6 +1434,9 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
 
   const Plan sp = plan_gemm(M, N, K_phys, group_rows, kmap != nullptr, regime, kinv != nullptr, lda);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
+  if (ws.scratch_cap > 0 && need > ws.scratch_cap)
+    return fail(OC_ERR_WORKSPACE, "this call needs %zu bytes of scratch; the static scratch holds %zu", need,
+                ws.scratch_cap);
   if (need > 0) {
     if (!workspace || workspace_bytes_given < need)
       return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
@@ -1484,6 +1489,20 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   else launch_gptq<OC_DTYPE_F16, OC_DTYPE_F16>(p, sp, s);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
+}
+
+}  // namespace oc
+
+extern "C" {
+
+int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
+                 const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
+                 int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
+                 int32_t bias_dtype, void *c, int64_t ldc, void *workspace, size_t workspace_bytes_given,
+                 int32_t regime, void *stream) {
+  clear_error();
+  return gemm_impl(a, lda, a_dtype, M, K_logical, qt, st, scale_dtype, zt, N, K_phys, group_rows, kmap, kinv,
+                   bias, bias_dtype, c, ldc, WorkspaceArg{workspace, workspace_bytes_given, 0}, regime, stream);
 }
 
 int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_t K, const uint8_t *qweight_u8,

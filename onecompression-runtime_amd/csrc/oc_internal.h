@@ -37,6 +37,27 @@ inline bool aligned(const void *p, size_t bytes) {
   return (reinterpret_cast<uintptr_t>(p) % bytes) == 0;
 }
 
+// GEMM workspace layout, every regime: [counter area][gathered activations]
+// [fp32 partials]. The counter area holds the small-batch kernels' arrival
+// counters and swap cells; it must be zero when a workspace is first used and
+// every call leaves it zero, so no regime writes anything else there.
+constexpr size_t COUNTER_BYTES = 512 * 1024;
+
+// Workspace of one GEMM call: the caller's buffer, or (scratch_cap > 0) a
+// static scratch array whose capacity bounds the call.
+struct WorkspaceArg {
+  void *ptr;
+  size_t bytes;
+  size_t scratch_cap;
+};
+
+// The body of oc_int4_gemm (oc_gemm.hip), shared by the entry points that
+// bring their own workspace and by the allocation-free one.
+int gemm_impl(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
+              const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
+              int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
+              int32_t bias_dtype, void *c, int64_t ldc, WorkspaceArg ws, int32_t regime, void *stream);
+
 }  // namespace oc
 
 // Returns OC_ERR_HIP (with the HIP error string) from the enclosing function

@@ -102,6 +102,66 @@ __global__ __launch_bounds__(256) void dequant_tiled_kernel(const uint32_t *__re
   else static_cast<uint16_t *>(out)[o] = static_cast<uint16_t>(pack2<ODT>(v, 0.f));
 }
 
+// Checkpoint-format words from the tiled layout (the inverse of
+// prepare_words_kernel). One thread per output word (r, n) of
+// qweight [ceil(out_rows / 8), N]: code row k = 8r + i is physical row
+// row_src[k] (or k without a map); rows past out_rows, rows whose source is
+// -1 and sources past K_phys give zero codes.
+__global__ __launch_bounds__(256) void export_words_kernel(const uint32_t *__restrict__ qt, int KS,
+                                                           const int32_t *__restrict__ row_src, int out_rows, int N,
+                                                           uint32_t *__restrict__ qweight) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int rows8 = (out_rows + 7) / 8;
+  if (idx >= static_cast<int64_t>(rows8) * N) return;
+  const int n = static_cast<int>(idx % N);
+  const int r = static_cast<int>(idx / N);
+  const int t = n / TILE_N, c = n % TILE_N;
+  const int K_phys = 32 * KS;
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int k = 8 * r + i;
+    if (k >= out_rows) break;
+    const int kp = row_src ? row_src[k] : k;
+    if (kp < 0 || kp >= K_phys) continue;
+    const uint32_t w = qt[((static_cast<int64_t>(t) * KS + kp / 32) * TILE_N + c) * 4 + ((kp >> 3) & 3)];
+    word |= ((w >> (4 * (kp & 7))) & 0xFu) << (4 * i);
+  }
+  qweight[idx] = word;
+}
+
+// One thread per qzeros word (g, n / 8) and the 8 scales beside it. Groups
+// past the layer's G are written as zero scales and zero stored zeros (the
+// reference's K padding); a v1 checkpoint stores zero - 1 (mod 16).
+__global__ __launch_bounds__(256) void export_meta_kernel(const uint16_t *__restrict__ st,
+                                                          const uint32_t *__restrict__ zt, int G, int out_groups,
+                                                          int N, int zero_mode, uint16_t *__restrict__ scales,
+                                                          uint32_t *__restrict__ qzeros) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int words = N / 8;
+  if (idx >= static_cast<int64_t>(out_groups) * words) return;
+  const int g = static_cast<int>(idx / words);
+  const int n0 = 8 * static_cast<int>(idx % words);
+  const int t = n0 / TILE_N, c0 = n0 % TILE_N;
+  uint32_t zout = 0;
+  uint16_t sv[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  if (g < G) {
+    const int64_t tg = static_cast<int64_t>(t) * G + g;
+    const uint32_t zw = zt[tg * 2 + (c0 >> 3)];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t z = (zw >> (4 * j)) & 0xFu;
+      if (zero_mode == OC_ZERO_V1) z = (z + 15u) & 0xFu;
+      zout |= z << (4 * j);
+      sv[j] = st[tg * TILE_N + c0 + j];
+    }
+  }
+  qzeros[idx] = zout;
+  uint16_t *srow = scales + static_cast<int64_t>(g) * N + n0;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) srow[j] = sv[j];
+}
+
 }  // namespace
 
 namespace {
@@ -207,6 +267,30 @@ int oc_int4_prepare(const int32_t *qweight, int32_t K, int32_t N, const int32_t 
   hipLaunchKernelGGL(prepare_meta_kernel, dim3(grid_of(metas)), dim3(256), 0, s,
                      static_cast<const uint16_t *>(scales), qzeros, zero_mode, N, G, tiles,
                      static_cast<uint16_t *>(st), reinterpret_cast<uint32_t *>(zt));
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_int4_export(const int32_t *qt, const void *st, const int32_t *zt, int32_t N, int32_t K_phys,
+                   int32_t group_rows, const int32_t *row_src, int32_t out_rows, int32_t out_groups,
+                   int32_t zero_mode, int32_t *qweight, void *scales, int32_t *qzeros, void *stream) {
+  clear_error();
+  if (!qt || !st || !zt || !qweight || !scales || !qzeros) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (zero_mode != OC_ZERO_V1 && zero_mode != OC_ZERO_V2)
+    return fail(OC_ERR_INVALID_ARGUMENT, "zero_mode must be OC_ZERO_V1 or OC_ZERO_V2");
+  if (N <= 0 || N % 8 != 0 || K_phys <= 0 || K_phys % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 ||
+      K_phys % group_rows != 0 || out_rows <= 0 || out_groups <= 0)
+    return fail(OC_ERR_SHAPE, "bad shape N=%d K_phys=%d group_rows=%d out_rows=%d out_groups=%d", N, K_phys,
+                group_rows, out_rows, out_groups);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t words = static_cast<int64_t>((out_rows + 7) / 8) * N;
+  hipLaunchKernelGGL(export_words_kernel, dim3(grid_of(words)), dim3(256), 0, s,
+                     reinterpret_cast<const uint32_t *>(qt), K_phys / 32, row_src, out_rows, N,
+                     reinterpret_cast<uint32_t *>(qweight));
+  const int64_t metas = static_cast<int64_t>(out_groups) * (N / 8);
+  hipLaunchKernelGGL(export_meta_kernel, dim3(grid_of(metas)), dim3(256), 0, s, static_cast<const uint16_t *>(st),
+                     reinterpret_cast<const uint32_t *>(zt), K_phys / group_rows, out_groups, N, zero_mode,
+                     static_cast<uint16_t *>(scales), reinterpret_cast<uint32_t *>(qzeros));
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }

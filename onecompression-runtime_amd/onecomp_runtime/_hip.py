@@ -71,6 +71,10 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _I32, _I32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _P, _P],
     ),
+    "oc_int4_export": (
+        ctypes.c_int,
+        [_P, _P, _P, _I32, _I32, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P],
+    ),
     "oc_int4_dequant_tiled": (
         ctypes.c_int,
         [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _P, _I32, _P],
@@ -190,29 +194,37 @@ def stream_of(device: torch.device | int) -> int:
 
 
 class _Workspace:
-    """Per-device scratch: gathered activations and split-K partials.
+    """Scratch of the GEMM calls (counter area, gathered activations, split-K
+    partials), one buffer per (device, stream).
 
-    One workspace serves every call issued on one stream (each call
-    overwrites the partials it reads); it grows on demand. Run a layer once
-    eagerly before a graph capture so captured launches never grow it.
+    Calls on one stream run in order, so they can share a buffer (each call
+    overwrites what it reads and leaves the counter area zero); calls on
+    different streams may overlap in time, so every stream gets its own.
+    A graph captured on a stream keeps that stream's buffer address: graphs
+    replayed concurrently must be captured on distinct streams. Buffers grow
+    on demand; outgrown ones stay allocated, since a captured graph may still
+    hold their address. The first call on a stream allocates, so run each
+    layer once on the capture stream (or eagerly on it) before a capture if
+    the capture must not allocate.
     """
 
     def __init__(self) -> None:
-        self._bufs: dict[int, torch.Tensor] = {}
-        # Outgrown buffers stay allocated: a captured graph may still hold their address.
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
         self._retired: list[torch.Tensor] = []
 
-    def get(self, device: torch.device | int, nbytes: int) -> torch.Tensor | None:
+    def get(self, device: torch.device | int, nbytes: int, stream: int | None = None) -> torch.Tensor | None:
         if nbytes == 0:
             return None
         idx = device if isinstance(device, int) else (
             device.index if device.index is not None else torch.cuda.current_device())
-        buf = self._bufs.get(idx)
+        key = (idx, _raw_stream(idx) if stream is None else stream)
+        buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
             if buf is not None:
                 self._retired.append(buf)
+            # zero-filled: the counter area must start at zero
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=torch.device("cuda", idx))
-            self._bufs[idx] = buf
+            self._bufs[key] = buf
         return buf
 
 
@@ -225,6 +237,6 @@ def gemm_workspace_bytes(M: int, N: int, K_phys: int, group_rows: int, has_kmap:
 
 
 def gemm_workspace(device: torch.device | int, M: int, N: int, K_phys: int, group_rows: int,
-                   has_kmap: bool, regime: int):
+                   has_kmap: bool, regime: int, stream: int | None = None):
     nbytes = gemm_workspace_bytes(M, N, K_phys, group_rows, has_kmap, regime)
-    return workspace.get(device, nbytes), nbytes
+    return workspace.get(device, nbytes, stream), nbytes

@@ -93,14 +93,6 @@ def can_use_fused_padded_groups(entry: dict[str, Any]) -> bool:
     )
 
 
-def is_ffn_layer(entry: dict[str, Any]) -> bool:
-    return ".ffn." in str(entry.get("name", ""))
-
-
-def is_ffn_up_layer(entry: dict[str, Any]) -> bool:
-    return ".ffn.net.0.proj" in str(entry.get("name", ""))
-
-
 def resolve_backend(backend: str | None, use_fused: bool = True) -> str:
     """Pick the int4 GEMM backend (reference: backend.py:103-144).
 

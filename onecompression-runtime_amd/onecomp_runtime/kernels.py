@@ -121,6 +121,29 @@ def prepare(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, *
     return TiledWeights(qt, st, zt, N, int(k_phys), int(group_rows))
 
 
+def export_checkpoint(w: TiledWeights, *, row_src: torch.Tensor | None, out_rows: int, out_groups: int,
+                      v1: bool) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Checkpoint-format ``(qweight, scales, qzeros)`` from the tiled layout
+    (``oc_int4_export``): qweight int32 [ceil(out_rows/8), N], code row k taken
+    from physical row ``row_src[k]`` (identity when None); scales [out_groups, N]
+    in the tiled scales' dtype; qzeros int32 [out_groups, N/8], v1 storing
+    zero - 1. Rows and groups past the layer are zero."""
+    dev = require_device(w.qt, row_src)
+    if row_src is not None and (row_src.dtype != torch.int32 or row_src.numel() < out_rows):
+        raise ValueError(f"row_src must be int32 with {out_rows} entries")
+    N = w.N
+    qweight = torch.empty(((out_rows + 7) // 8, N), dtype=torch.int32, device=dev)
+    scales = torch.empty((out_groups, N), dtype=w.st.dtype, device=dev)
+    qzeros = torch.empty((out_groups, N // 8), dtype=torch.int32, device=dev)
+    check(
+        lib().oc_int4_export(ptr(w.qt), ptr(w.st), ptr(w.zt), N, w.k_phys, w.group_rows, ptr(row_src),
+                             int(out_rows), int(out_groups), _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2,
+                             ptr(qweight), ptr(scales), ptr(qzeros), stream_of(dev)),
+        "oc_int4_export",
+    )
+    return qweight, scales, qzeros
+
+
 def dequant_tiled(w: TiledWeights, kmap: torch.Tensor | None, in_features: int,
                   dtype: torch.dtype) -> torch.Tensor:
     """Dense [N, in_features] weight (original K order) from the tiled layout."""
@@ -203,14 +226,14 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
     N = w.N
     if out is None:
         out = torch.empty((M, N), dtype=adt, device=a_2d.device)
-    ws, nbytes = _hip.gemm_workspace(idx, M, N, w.k_phys, w.group_rows, kmap is not None, regime)
+    stream = _hip._raw_stream(idx)
+    ws, nbytes = _hip.gemm_workspace(idx, M, N, w.k_phys, w.group_rows, kmap is not None, regime, stream)
     status = _gemm_fn()(
         a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, in_features, qt.data_ptr(), w.st.data_ptr(),
         _DT[w.st.dtype], w.zt.data_ptr(), N, w.k_phys, w.group_rows,
         None if kmap is None else kmap.data_ptr(), None if kinv is None else kinv.data_ptr(),
         None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
-        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes, regime,
-        _hip.stream_of(idx),
+        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes, regime, stream,
     )
     if status:
         check(status, "oc_int4_gemm")

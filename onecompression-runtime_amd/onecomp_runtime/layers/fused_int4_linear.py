@@ -15,17 +15,61 @@ steps are 256 contiguous bytes, with the tile's scales and zeros (restored
 to their value, so v1 and v2 checkpoints run the same kernels) beside them.
 The layer keeps only the tiled tensors (``qweight_tiled``, ``scales_tiled``,
 ``zeros_tiled``); checkpoint-format tensors given on the CPU are held until
-the first device forward prepares them.
+the first device forward prepares them. ``state_dict`` / ``load_state_dict``
+and the ``qweight`` / ``scales`` / ``qzeros`` attributes use the reference
+modules' buffer layouts, translated to and from the tiled one on the device.
 """
 from __future__ import annotations
+
+import collections
+import weakref
 
 import torch
 
 from .. import _hip, _profile, kernels
 
 
+def _unpack_host(qweight: torch.Tensor, rows: int) -> torch.Tensor:
+    """int32 [R, N] packed along K -> int32 codes [rows, N] (host, load/save time)."""
+    q = qweight.to(torch.int64) & 0xFFFFFFFF
+    parts = [(q >> (4 * i)) & 0xF for i in range(8)]
+    return torch.stack(parts, dim=1).reshape(-1, q.shape[1])[:rows].to(torch.int32)
+
+
+def _pack_host(codes: torch.Tensor) -> torch.Tensor:
+    """int codes [K, N] -> int32 [ceil(K/8), N] packed along K (host, load/save time)."""
+    K, N = codes.shape
+    full = torch.zeros(((K + 7) // 8 * 8, N), dtype=torch.int64)
+    full[:K] = codes.to(torch.int64) & 0xF
+    full = full.reshape(-1, 8, N)
+    word = torch.zeros((full.shape[0], N), dtype=torch.int64)
+    for i in range(8):
+        word |= full[:, i, :] << (4 * i)
+    return torch.where(word >= 2**31, word - 2**32, word).to(torch.int32)
+
+
 class _HipGPTQLinear(torch.nn.Module):
-    """Shared state and forward of the packed GPTQ int4 layers."""
+    """Shared state and forward of the packed GPTQ int4 layers.
+
+    Device state is the tiled layout only (non-persistent buffers
+    ``qweight_tiled`` / ``scales_tiled`` / ``zeros_tiled`` plus the row maps).
+    The module's ``state_dict`` holds the reference module's buffers instead
+    -- ``qweight``, ``scales``, ``qzeros`` in the checkpoint formats and in the
+    layout the reference class registers (``_STATE_LAYOUT``) -- written from
+    the tiled layout by ``oc_int4_export``; ``load_state_dict`` takes the same
+    tensors and re-runs ``oc_int4_prepare``. ``.qweight`` / ``.scales`` /
+    ``.qzeros`` read back the same tensors.
+
+    ``_STATE_LAYOUT``:
+      "kpad256"  FusedInt4Linear: K padded to a multiple of 256 with zero rows,
+                 zero scales and zero stored zeros (fused_int4_linear.py:989-1005)
+      "physical" FusedInt4LinearPaddedGroups: the 32-row group slots
+                 (fused_int4_linear.py:796-803), i.e. the physical row order
+      "input"    PackedGPTQLinear / FusedInt4LinearAnyGroup: the checkpoint
+                 tensors as given (packed_gptq_linear.py:57-60)
+    """
+
+    _STATE_LAYOUT = "input"
 
     def _setup(self, in_features: int, out_features: int, qweight: torch.Tensor,
                scales: torch.Tensor, qzeros: torch.Tensor, bias: torch.Tensor | None,
@@ -35,52 +79,74 @@ class _HipGPTQLinear(torch.nn.Module):
         self.groupsize = int(groupsize)
         self.v1 = bool(v1)
         self._kind = kind
-        if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
-            raise ValueError("qweight and qzeros must be int32")
         if self.out_features % 8 != 0:
             raise ValueError(f"out_features must be a multiple of 8, got {self.out_features}")
-        if qweight.shape[1] != self.out_features:
-            raise ValueError(f"qweight has {qweight.shape[1]} columns, expected {self.out_features}")
-        rows_expected = (self.in_features + 7) // 8
-        if qweight.shape[0] < rows_expected:
-            raise ValueError(f"qweight K-dim mismatch: got {qweight.shape[0]}, expected {rows_expected}")
-        plan = kernels.plan_groups(self.in_features, self.groupsize, g_idx)
-        if scales.shape[0] < plan.num_groups or scales.shape[1] != self.out_features:
-            raise ValueError(f"scales shape {tuple(scales.shape)} does not cover "
-                             f"{plan.num_groups} groups x {self.out_features}")
-        if tuple(qzeros.shape[1:]) != (self.out_features // 8,) or qzeros.shape[0] < plan.num_groups:
-            raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover "
-                             f"{plan.num_groups} groups x {self.out_features // 8}")
-        self.k_phys = plan.k_phys
-        self.group_rows = plan.group_rows
-        self.num_phys_groups = plan.num_groups
-        if scales.dtype not in (torch.float16, torch.bfloat16):
-            scales = scales.to(torch.float16)
-        # The kernels read activations through kmap (physical -> input row) and
-        # kinv (input -> physical row) only when the rows moved.
-        kmap, kinv = kernels.row_maps(plan, qweight.device)
-        self.register_buffer("kmap", kmap, persistent=False)
-        self.register_buffer("kinv", kinv, persistent=False)
-        self.register_buffer("qweight_tiled", None)
-        self.register_buffer("scales_tiled", None)
-        self.register_buffer("zeros_tiled", None)
-        # Checkpoint-format tensors waiting for the first device forward.
-        self.register_buffer("_src_qweight", qweight, persistent=False)
-        self.register_buffer("_src_scales", scales, persistent=False)
-        self.register_buffer("_src_qzeros", qzeros, persistent=False)
+        for name in ("qweight_tiled", "scales_tiled", "zeros_tiled", "kmap", "kinv",
+                     "_src_qweight", "_src_scales", "_src_qzeros"):
+            self.register_buffer(name, None, persistent=False)
+        self._weights = None
+        self._configure(g_idx, qweight.device)
+        # Row and group counts of the checkpoint tensors as given (the "input"
+        # state layout reproduces them).
+        self._ckpt_rows = int(qweight.shape[0]) if qweight.dim() == 2 else 0
+        self._ckpt_groups = int(scales.shape[0]) if scales.dim() == 2 else 0
+        self._set_sources(qweight, scales, qzeros, physical=False)
         if bias is not None:
             self.register_buffer("bias", bias.contiguous())
         else:
             self.bias = None
+
+    def _configure(self, g_idx: torch.Tensor | None, device: torch.device) -> None:
+        """Plan the physical rows (``oc_int4_plan_groups``) and keep the row maps."""
+        plan = kernels.plan_groups(self.in_features, self.groupsize, g_idx)
+        self._plan = plan
+        self.k_phys = plan.k_phys
+        self.group_rows = plan.group_rows
+        self.num_phys_groups = plan.num_groups
+        # The kernels read activations through kmap (physical -> input row) and
+        # kinv (input -> physical row) only when the rows moved.
+        self.kmap, self.kinv = kernels.row_maps(plan, device)
+
+    def _check_sources(self, qweight, scales, qzeros, physical: bool) -> None:
+        if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
+            raise ValueError("qweight and qzeros must be int32")
+        if qweight.dim() != 2 or qweight.shape[1] != self.out_features:
+            raise ValueError(f"qweight has shape {tuple(qweight.shape)}, expected [*, {self.out_features}]")
+        rows_expected = (self.k_phys if physical else self.in_features + 7) // 8
+        if qweight.shape[0] < rows_expected:
+            raise ValueError(f"qweight K-dim mismatch: got {qweight.shape[0]}, expected {rows_expected}")
+        G = self.num_phys_groups
+        if scales.dim() != 2 or scales.shape[0] < G or scales.shape[1] != self.out_features:
+            raise ValueError(f"scales shape {tuple(scales.shape)} does not cover "
+                             f"{G} groups x {self.out_features}")
+        if qzeros.dim() != 2 or tuple(qzeros.shape[1:]) != (self.out_features // 8,) or qzeros.shape[0] < G:
+            raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover "
+                             f"{G} groups x {self.out_features // 8}")
+
+    def _set_sources(self, qweight, scales, qzeros, *, physical: bool) -> None:
+        """Checkpoint tensors (input row order, or ``physical`` row order) to be
+        written into the tiled layout: now when on the device, else at the
+        first device forward."""
+        self._check_sources(qweight, scales, qzeros, physical)
+        if scales.dtype not in (torch.float16, torch.bfloat16):
+            scales = scales.to(torch.float16)
+        self._src_qweight, self._src_scales, self._src_qzeros = qweight, scales, qzeros
+        self._src_physical = physical
+        self.qweight_tiled = self.scales_tiled = self.zeros_tiled = None
         self._weights = None
         if qweight.is_cuda:
             self._prepare()
 
     def _prepare(self) -> kernels.TiledWeights:
         """Write the tiled layout on the layer's device and drop the sources."""
-        w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
-                            in_features=self.in_features, out_features=self.out_features,
-                            kmap=self.kmap, k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
+        if self._src_physical:  # rows already in physical order: identity map
+            w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
+                                in_features=self.k_phys, out_features=self.out_features, kmap=None,
+                                k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
+        else:
+            w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
+                                in_features=self.in_features, out_features=self.out_features,
+                                kmap=self.kmap, k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
         self.qweight_tiled, self.scales_tiled, self.zeros_tiled = w.qt, w.st, w.zt
         self._src_qweight = self._src_scales = self._src_qzeros = None
         self._weights = w
@@ -100,7 +166,114 @@ class _HipGPTQLinear(torch.nn.Module):
             self._weights = w
         return w
 
-    def _gemm(self, x: torch.Tensor) -> torch.Tensor:
+    # ---- reference module state -------------------------------------------------
+    def _state_shape(self) -> tuple[int, int]:
+        """(code rows, groups) of the reference buffers of this class."""
+        if self._STATE_LAYOUT == "kpad256":
+            k_pad = (self.in_features + 255) // 256 * 256
+            return k_pad, k_pad // self.groupsize
+        if self._STATE_LAYOUT == "physical":
+            return self.k_phys, max(self._ckpt_groups, self.num_phys_groups)
+        return max(8 * self._ckpt_rows, self.in_features), max(self._ckpt_groups, self.num_phys_groups)
+
+    def checkpoint_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """``(qweight, scales, qzeros)`` as the reference module holds them."""
+        rows, groups = self._state_shape()
+        if self.qweight_tiled is None and self._src_qweight is not None and not self._src_qweight.is_cuda:
+            return self._host_checkpoint(rows, groups)
+        w = self.tiled()
+        row_src = None
+        if self._STATE_LAYOUT == "input" and not self._plan.identity:
+            live = self._plan.kmap >= 0
+            inv = torch.full((rows,), -1, dtype=torch.int32)
+            inv[torch.from_numpy(self._plan.kmap[live]).long()] = torch.from_numpy(
+                live.nonzero()[0].astype("int32"))
+            row_src = inv.to(w.qt.device)
+        return kernels.export_checkpoint(w, row_src=row_src, out_rows=rows, out_groups=groups, v1=self.v1)
+
+    def _host_checkpoint(self, rows: int, groups: int):
+        """The same tensors from sources still held on the host (before the
+        first device move): integer re-layout only."""
+        q, s, z = self._src_qweight, self._src_scales, self._src_qzeros
+        N = self.out_features
+
+        def fit(t, n, cols):
+            out = torch.zeros((n, cols), dtype=t.dtype)
+            m = min(n, t.shape[0])
+            out[:m] = t[:m]
+            return out
+
+        if self._src_physical or self._STATE_LAYOUT == "input":
+            return q, s, z
+        if self._STATE_LAYOUT == "physical":
+            codes = _unpack_host(q, self.in_features)
+            kmap = torch.from_numpy(self._plan.kmap).long()
+            phys = torch.zeros((self.k_phys, N), dtype=torch.int32)
+            live = kmap >= 0
+            phys[live] = codes[kmap[live]]
+            return _pack_host(phys), s, z
+        # kpad256: zero rows, scales and stored zeros past in_features
+        G = (self.in_features + self.groupsize - 1) // self.groupsize
+        return (fit(fit(q, (self.in_features + 7) // 8, N), rows // 8, N), fit(fit(s, G, N), groups, N),
+                fit(fit(z, G, N // 8), groups, N // 8))
+
+    @property
+    def qweight(self) -> torch.Tensor:
+        return self.checkpoint_tensors()[0]
+
+    @property
+    def scales(self) -> torch.Tensor:
+        return self.checkpoint_tensors()[1]
+
+    @property
+    def qzeros(self) -> torch.Tensor:
+        return self.checkpoint_tensors()[2]
+
+    def _save_to_state_dict(self, destination, prefix, keep_vars):
+        q, s, z = self.checkpoint_tensors()
+        destination[prefix + "qweight"] = q
+        destination[prefix + "scales"] = s
+        destination[prefix + "qzeros"] = z
+        super()._save_to_state_dict(destination, prefix, keep_vars)
+
+    def _load_from_state_dict(self, state_dict, prefix, local_metadata, strict, missing_keys,
+                              unexpected_keys, error_msgs):
+        keys = [prefix + n for n in ("qweight", "scales", "qzeros")]
+        present = [k in state_dict for k in keys]
+        if all(present):
+            try:
+                g_key = prefix + "g_idx"
+                g_idx = state_dict.get(g_key) if "g_idx" in self._buffers else None
+                self.load_checkpoint(*(state_dict[k] for k in keys), g_idx=g_idx)
+            except (ValueError, RuntimeError) as e:
+                error_msgs.append(f"{prefix}: {e}")
+        elif strict:
+            missing_keys.extend(k for k, p in zip(keys, present) if not p)
+        super()._load_from_state_dict(state_dict, prefix, local_metadata, strict, missing_keys,
+                                      unexpected_keys, error_msgs)
+        for k in keys:
+            if k in unexpected_keys:
+                unexpected_keys.remove(k)
+
+    def load_checkpoint(self, qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor,
+                        g_idx: torch.Tensor | None = None) -> None:
+        """Replace the weights by reference-layout tensors (as ``state_dict``
+        holds them) and rebuild the tiled layout on the layer's device."""
+        ref = self.qweight_tiled if self.qweight_tiled is not None else self._src_qweight
+        device = ref.device
+        if g_idx is not None:
+            self._configure(g_idx, device)
+        physical = self._STATE_LAYOUT == "physical"
+        if self._STATE_LAYOUT == "input":
+            self._ckpt_rows = int(qweight.shape[0])
+            self._ckpt_groups = int(scales.shape[0])
+        dt = self.scales_tiled.dtype if self.scales_tiled is not None else self._src_scales.dtype
+        self._set_sources(qweight.to(device), scales.to(device=device, dtype=dt), qzeros.to(device),
+                          physical=physical)
+
+    # ---- forward ----------------------------------------------------------------
+
+    def _gemm(self, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         orig_dtype = x.dtype
         if orig_dtype == torch.float32:
             # fp32 input is computed in fp16 and returned as fp32
@@ -110,14 +283,15 @@ class _HipGPTQLinear(torch.nn.Module):
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
         c = kernels.int4_gemm(a_2d, self.tiled(), in_features=self.in_features, kmap=self.kmap,
-                              kinv=self.kinv, bias=self.bias)
+                              kinv=self.kinv, bias=bias)
         out = c.reshape(*x.shape[:-1], self.out_features)
         if orig_dtype == torch.float32:
             out = out.to(torch.float32)
         return out
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        return self._gemm(x)
+        # The reference's fused kernels add the bias buffer as stored, in fp32.
+        return self._gemm(x, self.bias)
 
     def dequantize(self, dtype: torch.dtype = torch.float16) -> torch.Tensor:
         """Dense [out_features, in_features] weight, values as the reference's
@@ -172,14 +346,19 @@ class FusedInt4Linear(_HipGPTQLinear):
 
     Constructor and attributes as the reference (fused_int4_linear.py:966-1014);
     ``v1`` (keyword) selects the zero convention of the checkpoint format,
-    "gptq" (v1, the reference's only mode) or "gptq_v2".
+    "gptq" (v1, the reference's only mode) or "gptq_v2". Its state holds the
+    reference's K-padded buffers (K rounded up to 256, zero rows/scales/zeros).
     """
+
+    _STATE_LAYOUT = "kpad256"
 
     def __init__(self, in_features: int, out_features: int, qweight: torch.Tensor,
                  scales: torch.Tensor, qzeros: torch.Tensor, bias: torch.Tensor | None = None,
                  groupsize: int = 32, *, v1: bool = True):
         super().__init__()
         assert groupsize == 32, "FusedInt4Linear supports groupsize=32 only"
+        # K of the reference's registered buffers (padded to a multiple of 256)
+        self._k_padded = (int(in_features) + 255) // 256 * 256
         self._setup(in_features, out_features, qweight, scales, qzeros, bias, 32, None, v1, "fused")
 
     @classmethod
@@ -196,8 +375,11 @@ class FusedInt4Linear(_HipGPTQLinear):
 class FusedInt4LinearPaddedGroups(_HipGPTQLinear):
     """Odd groupsize (< 32) GPTQ int4 layer, re-laid into 32-row groups.
 
-    Same constructor checks as the reference (fused_int4_linear.py:770-811).
+    Same constructor checks as the reference (fused_int4_linear.py:770-811);
+    its state holds the 32-row-slot qweight the reference registers (:796-803).
     """
+
+    _STATE_LAYOUT = "physical"
 
     def __init__(self, in_features: int, out_features: int, qweight: torch.Tensor,
                  scales: torch.Tensor, qzeros: torch.Tensor, bias: torch.Tensor | None = None,
@@ -224,6 +406,35 @@ class FusedInt4LinearAnyGroup(_HipGPTQLinear):
         super().__init__()
         self._setup(in_features, out_features, qweight, scales, qzeros, bias, groupsize, None, v1,
                     "any_group")
+
+
+_TILE_CACHE: "collections.OrderedDict[tuple, tuple]" = collections.OrderedDict()
+_TILE_CACHE_MAX = 64
+
+
+def _functional_tiles(qweight, scales, qzeros, K: int, N: int) -> kernels.TiledWeights:
+    """Tiled layout of the functional form's weights, cached per tensor triple.
+
+    The functional API has no load step; the tiled layout is written on the
+    first call and reused while the same tensor objects, unmodified (their
+    version counters), come back. Entries hold weak references, so a freed
+    tensor whose address is reused never hits a stale entry.
+    """
+    key = (qweight.data_ptr(), scales.data_ptr(), qzeros.data_ptr(), scales.dtype, K, N)
+    ver = (qweight._version, scales._version, qzeros._version)
+    hit = _TILE_CACHE.get(key)
+    if hit is not None:
+        refs, v, w = hit
+        if refs[0]() is qweight and refs[1]() is scales and refs[2]() is qzeros and v == ver:
+            _TILE_CACHE.move_to_end(key)
+            return w
+        del _TILE_CACHE[key]
+    w = kernels.prepare(qweight.contiguous(), scales.contiguous(), qzeros.contiguous(), in_features=K,
+                        out_features=N, kmap=None, k_phys=K, group_rows=32, v1=True)
+    _TILE_CACHE[key] = ((weakref.ref(qweight), weakref.ref(scales), weakref.ref(qzeros)), ver, w)
+    while len(_TILE_CACHE) > _TILE_CACHE_MAX:
+        _TILE_CACHE.popitem(last=False)
+    return w
 
 
 def fused_int4_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor,
@@ -257,11 +468,7 @@ def fused_int4_gemm(a: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor
     assert K % 32 == 0, f"K must be a multiple of 32 (groupsize), got K={K}"
     if bias is not None:
         bias = bias.to(a.dtype)
-    # The functional form has no load time: the tiled layout is written per
-    # call (one extra pass over the packed weight).
-    w = kernels.prepare(qweight.contiguous(), scales.contiguous(), qzeros.contiguous(), in_features=K,
-                        out_features=N, kmap=None, k_phys=K, group_rows=32, v1=True)
-    c = kernels.int4_gemm(a_2d, w, in_features=K, bias=bias)
+    c = kernels.int4_gemm(a_2d, _functional_tiles(qweight, scales, qzeros, K, N), in_features=K, bias=bias)
     out = c.reshape(*leading_shape, N)
     if orig_dtype == torch.float32:
         out = out.to(torch.float32)

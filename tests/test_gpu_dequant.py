@@ -15,7 +15,12 @@ DEV = "cuda:0"
     (4096, 4096, 32, True, False, torch.bfloat16, torch.float16),   # gptq_gs32_m16 weights
     (4096, 4096, 32, True, False, torch.float16, torch.float16),
     (3072, 3072, 32, False, False, torch.bfloat16, torch.float16),  # dit_large_m (v2)
-    (5120, 1024, 32, True, True, torch.bfloat16, torch.float16),    # act-order g_idx
+    (5120, 1024, 32, True, True, torch.bfloat16, torch.float16),    # act-order g_idx (decode shapes)
+    (5120, 5120, 32, True, True, torch.bfloat16, torch.float16),
+    (5120, 17408, 32, True, True, torch.bfloat16, torch.float16),
+    (17408, 5120, 32, True, True, torch.bfloat16, torch.float16),
+    (3072, 12288, 32, False, False, torch.bfloat16, torch.float16),  # the other DiT shapes (v2)
+    (12288, 3072, 32, False, False, torch.bfloat16, torch.float16),
     (1040, 3072, 26, True, False, torch.bfloat16, torch.float16),   # odd groups
     (1000, 64, 32, True, False, torch.bfloat16, torch.bfloat16),    # ragged K, bf16 scales
     (256, 64, 128, False, False, torch.float32, torch.float16),

@@ -100,8 +100,7 @@ def test_dit_large_m_v2(K, N):
     x = synthetic.activations(4096, K, seed=20281, outliers=True)
     mod = _module_for(layer)
     out = mod(x.to(DEV))
-    rows = slice(0, 4096) if K * N <= 3072 * 3072 else slice(0, 512)
-    assert_gemm_close(out[rows], _oracle_out(layer, x[rows]), f"dit K={K} N={N}")
+    assert_gemm_close(out, _oracle_out(layer, x), f"dit K={K} N={N}")
 
 
 def test_padded_gs26():

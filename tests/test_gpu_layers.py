@@ -48,6 +48,33 @@ def test_rtn_linear_one_hot_bit_exact(M, G):
     assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, torch.bfloat16))
 
 
+@pytest.mark.parametrize("N", [24, 40])
+@pytest.mark.parametrize("M", [1, 65, 200])
+def test_rtn_linear_ragged_tile_n(N, M):
+    """N % 16 == 8: the last 16-column tile is half full (its upper lanes'
+    weight rows are clamped, never read past the table)."""
+    from onecomp_runtime import PackedRTNLinear
+
+    rng = np.random.default_rng(N * 1000 + M)
+    K, G = 256, 2
+    q = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    s = (np.abs(rng.standard_normal((N, G))) * 0.05 + 1e-3).astype(np.float16)
+    z = rng.integers(0, 16, (N, G)).astype(np.float16)
+    mod = PackedRTNLinear(K, N, torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV),
+                          torch.from_numpy(z).to(DEV))
+    assert mod._fused_ok(torch.zeros(1, K, dtype=torch.bfloat16))
+    wd = O.rtn_dequant(q, s.astype(np.float32), z.astype(np.float32), K, N, "bf16")
+    ks = rng.integers(0, K, M)
+    x = torch.zeros((M, K), dtype=torch.bfloat16)
+    x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+    say(f"rtn ragged tile N={N} M={M} one-hot")
+    assert np.array_equal(bits16(mod(x.to(DEV))), oracle_bits(wd[:, ks].T, torch.bfloat16))
+    xr = torch.randn(M, K, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
+    say(f"rtn ragged tile N={N} M={M} random")
+    ref = O.rtn_linear(np32(xr), q, s.astype(np.float32), z.astype(np.float32), K, N, "bf16")
+    assert_gemm_close(mod(xr.to(DEV)), ref, f"rtn N={N} M={M}")
+
+
 def test_rtn_linear_bias_and_fp32_path():
     from onecomp_runtime import PackedRTNLinear, synthetic
 
@@ -187,6 +214,32 @@ def test_moe_grouped_gemm(E, K, N, T, topk):
     assert_gemm_close(y, ref, "moe")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_moe_grouped_gemm_one_hot_bit_exact(dtype):
+    """In-kernel dequant of the grouped GEMM, bit for bit: token t's row is
+    e_{k_t}, so Y[t*topk + j] = Wd_{e(t,j)}[:, k_t]. Skewed routing: expert 0
+    takes every token (300 rows: three 128-row blocks, the last partial),
+    experts 1-3 share the second slot, experts 4-7 get no rows."""
+    from onecomp_runtime import kernels, synthetic
+
+    E, K, N, T, topk = 8, 512, 192, 300, 2
+    experts = synthetic.moe_experts(E, K, N, seed=20340)
+    ids = torch.stack([torch.zeros(T, dtype=torch.int64), 1 + torch.arange(T) % 3], dim=1)
+    rng = np.random.default_rng(20341)
+    ks = rng.integers(0, K, T)
+    x = torch.zeros((T, K), dtype=dtype)
+    x[torch.arange(T), torch.from_numpy(ks)] = 1.0
+    say(f"moe one-hot E={E} T={T} {dtype}")
+    off, pairs = kernels.moe_route(ids.to(DEV), E)
+    assert off.cpu().tolist() == [0, 300, 400, 500, 600, 600, 600, 600, 600]
+    w = kernels.prepare_experts(experts.qweight.to(DEV), experts.scales.to(DEV), experts.qzeros.to(DEV))
+    y = kernels.int4_moe_gemm(x.to(DEV), topk, w, off, pairs)
+    name = "bf16" if dtype == torch.bfloat16 else "f16"
+    wds = {e: O.dequant_gptq(*layer_oracle_inputs(experts.layers[e]), K, N, name) for e in range(4)}
+    expect = np.stack([wds[int(ids[t, j])][:, ks[t]] for t in range(T) for j in range(topk)])
+    assert np.array_equal(bits16(y), oracle_bits(expect, dtype))
+
+
 # -- reference API surface -----------------------------------------------------
 def test_functional_fused_int4_gemm():
     from onecomp_runtime import fused_int4_gemm, synthetic
@@ -268,6 +321,43 @@ def test_packed_gptq_8bit_and_fp32():
     assert out.dtype == torch.float32
     a, b, c, g = layer_oracle_inputs(layer)
     assert_gemm_close(out, O.gptq_linear(xf.numpy(), a, b, c, g, 256, 64, "f32"), "fp32 packed")
+
+
+@pytest.mark.parametrize("M", [1, 6, 100])
+def test_packed_gptq_bias_rounded_to_activation_dtype(M):
+    """PackedGPTQLinear adds ``bias.to(x.dtype)`` (packed_gptq_linear.py:73):
+    with one-hot rows the output is RNE(Wd[:, k] + RNE_bf16(bias)) exactly.
+    FusedInt4Linear adds the stored bias as is (the reference's kernels do)."""
+    from onecomp_runtime import FusedInt4Linear, PackedGPTQLinear, synthetic
+
+    K, N = 512, 64
+    # Power-of-two scales: every s * (w - z) is exact in bf16, so the decode
+    # kernel's unrounded products and the dequantize-then-multiply order agree
+    # and the comparison isolates the bias rounding.
+    gen = torch.Generator().manual_seed(8)
+
+    def pow2_scales(layer):
+        layer.scales = torch.pow(2.0, -torch.randint(2, 9, layer.scales.shape, generator=gen).float()).half()
+        return layer
+
+    layer = pow2_scales(synthetic.gptq_layer(K, N, seed=96, act_order=True))
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(7)) * 3.0  # fp32
+    mod = PackedGPTQLinear(K, N, layer.qweight.to(DEV), layer.scales.to(DEV), layer.qzeros.to(DEV),
+                           g_idx=layer.g_idx.to(DEV), bias=bias.to(DEV), groupsize=32)
+    rng = np.random.default_rng(M)
+    ks = rng.integers(0, K, M)
+    x = torch.zeros((M, K), dtype=torch.bfloat16)
+    x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+    wd = O.dequant_gptq(*layer_oracle_inputs(layer), K, N, "bf16")
+    say(f"packed fp32 bias M={M}")
+    expect = O.round_to(wd[:, ks].T + O.round_to(bias.numpy(), "bf16")[None, :], "bf16")
+    assert np.array_equal(bits16(mod(x.to(DEV))), oracle_bits(expect, torch.bfloat16))
+    plain = pow2_scales(synthetic.gptq_layer(K, N, seed=97))
+    fmod = FusedInt4Linear(K, N, plain.qweight.to(DEV), plain.scales.to(DEV), plain.qzeros.to(DEV),
+                           bias=bias.to(DEV))
+    wd2 = O.dequant_gptq(*layer_oracle_inputs(plain), K, N, "bf16")
+    expect2 = O.round_to(wd2[:, ks].T + bias.numpy()[None, :], "bf16")
+    assert np.array_equal(bits16(fmod(x.to(DEV))), oracle_bits(expect2, torch.bfloat16))
 
 
 def test_module_dtype_moves_keep_packed_buffers():
