@@ -221,6 +221,33 @@ int oc_int4_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
                  void *workspace, size_t workspace_bytes, int32_t regime,
                  void *stream);
 
+/*
+ * Device: oc_int4_gemm without a workspace argument, for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). No counterpart in the reference. Same arguments, math
+ * and regimes as oc_int4_gemm; the scratch it needs (counter area, gathered
+ * activations, split-K partials) comes from a static device array of the
+ * library, oc_int4_gemm_noalloc_scratch_bytes() bytes (32 MiB) per device,
+ * held by every GPU the library runs on until the process ends. Calls whose
+ * scratch need exceeds it return OC_ERR_WORKSPACE. The call allocates nothing
+ * (no hipMalloc / hipFree / allocating library routine). Every call on one
+ * GPU shares that GPU's array: calls that overlap in time on one GPU (two
+ * streams, or a graph replay beside an eager call) race and must not be
+ * issued. The first call on a device looks the array up and clears its
+ * counter area with a kernel on `stream`.
+ */
+int oc_int4_gemm_noalloc(const void *a, int64_t lda, int32_t a_dtype,
+                         int32_t M, int32_t K_logical, const int32_t *qt,
+                         const void *st, int32_t scale_dtype,
+                         const int32_t *zt, int32_t N, int32_t K_phys,
+                         int32_t group_rows, const int32_t *kmap,
+                         const uint16_t *kinv, const void *bias,
+                         int32_t bias_dtype, void *c, int64_t ldc,
+                         int32_t regime, void *stream);
+
+/* Bytes of the static scratch behind oc_int4_gemm_noalloc (per device). */
+size_t oc_int4_gemm_noalloc_scratch_bytes(void);
+
 /* Workspace bytes oc_int4_gemm needs for this call shape (0 if none). */
 size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys,
                                     int32_t group_rows, int32_t has_kmap,

@@ -90,6 +90,12 @@ SIGNATURES = {
          _P, _I64, _P, _SZ, _I32, _P],
     ),
     "oc_int4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "oc_int4_gemm_noalloc": (
+        ctypes.c_int,
+        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _I32,
+         _P, _I64, _I32, _P],
+    ),
+    "oc_int4_gemm_noalloc_scratch_bytes": (_SZ, []),
     "oc_rtn_dequant": (
         ctypes.c_int,
         [_P, _I32, _I32, _P, _I32, _P, _I32, _I32, _I32, _P, _I32, _P],
