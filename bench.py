@@ -14,8 +14,10 @@ M=1) timed with HIP events on the launch stream; its ``traffic`` (HBM bytes
 per launch) is read from ``profiles/gemv_stream_k5120_n17408_traffic.json``,
 written from two rocprofv3 --pmc runs of this script (FETCH_SIZE, WRITE_SIZE)
 scaled by the same counters on a plain copy of known size, which this script
-also launches. ``cpu_baseline`` times the CPU oracle (numpy restatement of
-the reference's packed path) on one pass of the M=1 sweep.
+also launches. ``cpu_baseline`` times the reference's two CPU paths in torch
+on the host (oracle/cpu_paths.py: "packed" = dequantize per call + F.linear,
+"eager" = F.linear on a weight dequantized once) for every workload; each
+sub-result carries its CPU medians and the GPU speed-up over both paths.
 
     python bench.py [--steps K] [--warmup W] [--workloads all|decode,...]
 """
@@ -332,51 +334,170 @@ def moe_workload(dev, steps, warmup):
             "us_eager": ms_eager * 1e3}
 
 
-def cpu_baseline(budget_s: float):
-    """Oracle packed path (numpy dequant + fp32 GEMM) on the M=1 decode sweep,
-    column chunks spread over a thread pool of the host's cores."""
-    from concurrent.futures import ThreadPoolExecutor
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
+
+def cpu_baseline(max_s_per_case: float = 4.0):
+    """The reference's CPU paths in torch on the host (oracle/cpu_paths.py):
+    "packed" dequantizes the weight on every call then F.linear
+    (packed_gptq_linear.py:66-74, packed_linear.py:53-56); "eager" runs F.linear
+    on a weight dequantized once (backend.py:246-264). Same seeded inputs as the
+    GPU workloads; torch.set_num_threads(<CPUs this process may run on>); the
+    median of 5 timed calls after 2 warmups per case. The DiT and MoE cases run
+    on a stated sample (fewer rows / experts) and report rates per byte / flop."""
     import numpy as np
+    import torch
 
     from onecomp_runtime import synthetic
-    from oracle import onecomp_oracle as O
+    from oracle import cpu_paths as C
 
-    cores = min(16, os.cpu_count() or 1)
-    layers = []
-    for i, (K, N) in enumerate(DECODE_SHAPES):
-        layer = synthetic.gptq_layer(K, N, seed=20270 + i, act_order=True)
-        x = synthetic.activations(1, K, seed=20272).float().numpy()
-        layers.append((K, N, layer.qweight.numpy(), layer.scales.float().numpy(), layer.qzeros.numpy(),
-                       layer.g_idx.numpy(), x))
-        del layer
+    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    bf = torch.bfloat16
 
-    def run_chunk(args):
-        K, qw, sc, qz, g, x, n0, n1 = args
-        n8 = slice(n0 // 8, n1 // 8)
-        return O.gptq_linear(x, qw[:, n0:n1], sc[:, n0:n1], qz[:, n8], g, K, n1 - n0, "bf16")
+    def median_s(fn, n=5, warm=2):
+        for _ in range(warm):
+            fn()
+        ts = []
+        for _ in range(n):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts))
 
-    def one_pass(pool):
-        for K, N, qw, sc, qz, g, x in layers:
-            step = max(8, (N // cores) // 8 * 8)
-            chunks = [(K, qw, sc, qz, g, x, n0, min(N, n0 + step)) for n0 in range(0, N, step)]
-            np.concatenate(list(pool.map(run_chunk, chunks)), axis=1)
+    def gptq(K, N, seed, **kw):
+        lay = synthetic.gptq_layer(K, N, seed=seed, **kw)
+        g = lay.g_idx if lay.g_idx is not None else torch.arange(K) // lay.groupsize
+        return C.PackedGPTQ(lay.qweight, lay.scales, lay.qzeros, g, K, N, bf, lay.v1)
 
-    with ThreadPoolExecutor(cores) as pool:
-        one_pass(pool)  # warm
-        t0 = time.perf_counter()
-        passes = 0
-        while True:
-            one_pass(pool)
-            passes += 1
-            if time.perf_counter() - t0 > budget_s / 2 or passes >= 5:
-                break
-        dt = (time.perf_counter() - t0) / passes
-    wbytes = sum(gptq_bytes(K, N) for K, N in DECODE_SHAPES)
-    return {"value": round(wbytes / dt / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"{passes} pass(es) of the M=1 act-order decode sweep (4 shapes, "
-                      f"{wbytes/1e6:.0f} MB packed weights): oracle packed path, numpy dequant + "
-                      f"fp32 GEMM per call, {cores} threads over column chunks; {dt*1e3:.0f} ms/pass"}
+    def both(make_calls, nbytes=None, flops=None, sample=None):
+        """make_calls() -> (packed step, eager step); rates from the medians."""
+        packed, eager = make_calls()
+        out = {}
+        with torch.no_grad():
+            for name, fn in (("packed", packed), ("eager", eager)):
+                t = median_s(fn)
+                r = {"ms": round(t * 1e3, 3)}
+                if nbytes:
+                    r["weight_GBps"] = round(nbytes / t / 1e9, 4)
+                if flops:
+                    r["TFLOPs"] = round(flops / t / 1e12, 5)
+                out[name] = r
+        if sample:
+            out["sample"] = sample
+        return out
+
+    res = {}
+    for M in (1, 8):
+        log(f"cpu: decode sweep M={M}")
+        mods = [gptq(K, N, seed=20270 + i, act_order=True) for i, (K, N) in enumerate(DECODE_SHAPES)]
+        eag = [m.eager() for m in mods]
+        xs = [synthetic.activations(M, K, seed=20271 + M) for K, _ in DECODE_SHAPES]
+        wb = sum(gptq_bytes(K, N) for K, N in DECODE_SHAPES)
+        fl = sum(2 * M * K * N for K, N in DECODE_SHAPES)
+        res[f"decode_actorder_m{M}"] = both(
+            lambda: (lambda: [m(x) for m, x in zip(mods, xs)], lambda: [e(x) for e, x in zip(eag, xs)]),
+            wb, fl, "one step = the 4 shapes")
+        del mods, eag
+    log("cpu: gs32 M=16")
+    m = gptq(4096, 4096, seed=20260)
+    x = synthetic.activations(16, 4096, seed=20261)
+    e = m.eager()
+    res["gptq_gs32_m16"] = both(lambda: (lambda: m(x), lambda: e(x)), gptq_bytes(4096, 4096), 2 * 16 * 4096 * 4096)
+    log("cpu: DiT (row sample)")
+    dit = {}
+    rows = 512
+    for i, (K, N) in enumerate(DIT_SHAPES):
+        m = gptq(K, N, seed=20280 + i, v1=False)
+        x = synthetic.activations(4096, K, seed=20281, outliers=True)[:rows]
+        e = m.eager()
+        dit[f"K{K}_N{N}"] = both(lambda: (lambda: m(x), lambda: e(x)), None, 2 * rows * K * N,
+                                 f"{rows} of the 4096 rows")
+    res["dit_large_m_m4096"] = dit
+    log("cpu: padded gs26")
+    lay = synthetic.gptq_layer(1040, 3072, seed=20290, groupsize=26, pad_rows_to=1056)
+    m = C.PackedGPTQ(lay.qweight, lay.scales, lay.qzeros, torch.arange(1040) // 26, 1040, 3072, bf, True)
+    x = synthetic.activations(256, 1040, seed=20291)
+    e = m.eager()
+    res["padded_gs26_m256"] = both(lambda: (lambda: m(x), lambda: e(x)), None, 2 * 256 * 1040 * 3072)
+    log("cpu: RTN linear / embedding")
+    rl = synthetic.rtn_layer(2048, 1024, seed=20300)
+    m = C.PackedRTN(rl.qweight_u8, rl.scales, rl.zeros, 1024, bf)
+    x = synthetic.activations(512, 1024, seed=20301)
+    e = m.eager()
+    res["rtn_linear_m512"] = both(lambda: (lambda: m(x), lambda: e(x)), None, 2 * 512 * 1024 * 2048)
+    V, D, T = 32768, 1024, 4096
+    for G in (1, 32):
+        el = synthetic.rtn_layer(V, D, seed=20310, groups=G)
+        ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311))
+        table = C.rtn_dequant(el.qweight_u8, el.scales, el.zeros, D, el.scales.dtype)
+        nbytes = T * (D // 2 + 4 * G) + T * 8 + T * D * 2
+        res[f"rtn_embedding_G{G}"] = both(
+            lambda: (lambda: C.embedding(ids, el.qweight_u8, el.scales, el.zeros, D), lambda: table[ids]),
+            nbytes, None, "eager = rows of a table dequantized once")
+        del el, table
+    log("cpu: MoE (expert sample)")
+    E, K, N, T, topk, sampled = 64, 4096, 2048, 512, 8, 8
+    ids = synthetic.router_topk(T, E, topk, seed=20332)
+    x = synthetic.activations(T, K, seed=20331)
+    flat = ids.reshape(-1)
+    experts = [C.PackedGPTQ(*(lambda l: (l.qweight, l.scales, l.qzeros, torch.arange(K) // 32))(
+        synthetic.gptq_layer(K, N, seed=20330 + 1000 * e)), K, N, bf, True) for e in range(sampled)]
+    eag = [p.eager() for p in experts]
+    pairs = [torch.nonzero(flat == e).flatten() for e in range(sampled)]
+
+    def moe(mods):
+        return [mods[e](x[pairs[e] // topk]) for e in range(sampled)]
+
+    res["moe_64x_top8"] = both(lambda: (lambda: moe(experts), lambda: moe(eag)), sampled * gptq_bytes(K, N),
+                               2 * sum(len(p) for p in pairs) * K * N,
+                               f"experts 0..{sampled - 1} of 64 with their routed rows")
+    head = res["decode_actorder_m1"]
+    return {
+        "value": head["packed"]["weight_GBps"], "unit": "GB/s", "cores": threads, "kind": "port",
+        "path": "packed", "eager_value": head["eager"]["weight_GBps"],
+        "cpu_model": cpu_model(), "os_cpu_count": os.cpu_count(), "torch_threads": torch.get_num_threads(),
+        "sample": "M=1 act-order decode sweep (4 shapes, packed weights per step); torch CPU, per call "
+                  "dequant + F.linear (packed); median of 5 after 2 warmups",
+        "per_config": res,
+    }
+
+
+def attach_cpu_ratios(sub: dict, head: dict, cpu: dict) -> None:
+    """Beside each GPU result: the CPU medians and GPU speed-up over each path."""
+    per = cpu["per_config"]
+
+    def put(dst: dict, src: dict, gpu_ms: float) -> None:
+        dst["cpu"] = src
+        for path in ("packed", "eager"):
+            dst[f"speedup_vs_cpu_{path}"] = round(src[path]["ms"] / gpu_ms, 1)
+
+    head["cpu"] = per["decode_actorder_m1"]
+    for path in ("packed", "eager"):
+        head[f"speedup_vs_cpu_{path}"] = round(per["decode_actorder_m1"][path]["ms"] / head["ms_per_step"], 1)
+    if "decode_actorder_m8" in sub:
+        put(sub["decode_actorder_m8"], per["decode_actorder_m8"], sub["decode_actorder_m8"]["ms_per_step"])
+    for key in ("gptq_gs32_m16", "padded_gs26_m256", "rtn_linear_m512", "rtn_embedding_G1", "rtn_embedding_G32"):
+        if key in sub:
+            put(sub[key], per[key], sub[key]["us"] / 1e3)
+    if "dit_large_m_m4096" in sub:
+        for shape, r in per["dit_large_m_m4096"].items():
+            g = sub["dit_large_m_m4096"][shape]
+            g["cpu"] = r
+            for path in ("packed", "eager"):
+                g[f"speedup_vs_cpu_{path}"] = round(g["TFLOPs"] / r[path]["TFLOPs"], 1)
+    if "moe_64x_top8" in sub:
+        g = sub["moe_64x_top8"]
+        g["cpu"] = per["moe_64x_top8"]
+        for path in ("packed", "eager"):
+            g[f"speedup_vs_cpu_{path}"] = round(g["weight_GBps"] / per["moe_64x_top8"][path]["weight_GBps"], 1)
 
 
 def main() -> int:
@@ -386,7 +507,6 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workloads", default="all",
                     help="comma list of: m16,dit,padded,rtn,moe (the headline always runs)")
-    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -444,8 +564,11 @@ def main() -> int:
 
     cpu = None
     if not args.no_cpu:
-        log("cpu baseline (oracle)")
-        cpu = cpu_baseline(args.cpu_seconds)
+        log("cpu baseline (torch CPU packed / eager paths)")
+        t0 = time.perf_counter()
+        cpu = cpu_baseline()
+        log(f"cpu baseline done in {time.perf_counter() - t0:.0f} s")
+        attach_cpu_ratios(sub, head, cpu)
 
     def rnd(o):
         if isinstance(o, float):
@@ -477,8 +600,10 @@ def main() -> int:
                    "ms_per_step_eager": round(head["ms_per_step_eager"], 5),
                    "weight_GBps_eager": round(head["weight_GBps_eager"], 2)},
         "roofline": roof,
-        "cpu_baseline": cpu,
+        "cpu_baseline": cpu and {k: v for k, v in cpu.items() if k != "per_config"},
         "hbm_frac_step": round(head["hbm_frac"], 4),
+        "headline_vs_cpu": head.get("cpu") and {k: head[k] for k in ("cpu", "speedup_vs_cpu_packed",
+                                                                     "speedup_vs_cpu_eager")},
         "sub_results": rnd(sub),
         "device": torch.cuda.get_device_name(dev),
     }

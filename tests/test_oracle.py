@@ -283,3 +283,78 @@ def test_gemm_close_rejects_planted_mistakes():
     assert not O.gemm_close(dropped, ref)[0]
     transposed = ref.T.copy().reshape(ref.shape)  # transposed operand
     assert not O.gemm_close(transposed, ref)[0]
+
+
+# -- the torch-CPU restatement used for the timed CPU baseline -----------------
+@pytest.mark.parametrize("case", ["gs32_v1", "actorder_v1", "gs26_v2", "gs128_8bit"])
+def test_cpu_paths_dequant_matches_oracle(case):
+    """oracle.cpu_paths dequantizes bit for bit like the numpy oracle."""
+    import torch
+
+    from oracle import cpu_paths as C
+
+    rng = np.random.default_rng(hash(case) % 1000)
+    K, N, gs, wbits, v1 = 200, 48, 32, 4, True
+    if case == "gs26_v2":
+        gs, v1 = 26, False
+    if case == "gs128_8bit":
+        gs, wbits = 128, 8
+    G = (K + gs - 1) // gs
+    codes = rng.integers(0, 1 << wbits, (K, N))
+    zeros = rng.integers(0, 1 << wbits, (G, N))
+    scales = (np.abs(rng.standard_normal((G, N))) * 0.01 + 1e-3).astype(np.float16)
+    g = rng.permutation(K) // gs if case == "actorder_v1" else O.default_g_idx(K, gs)
+    qw, qz = O.pack_rows(codes, wbits), O.pack_zeros(zeros, v1, wbits)
+    for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "f16"), (torch.float32, "f32")):
+        got = C.dequant_gptq(torch.from_numpy(qw), torch.from_numpy(scales), torch.from_numpy(qz),
+                             torch.from_numpy(g), K, N, dt, v1, wbits)
+        ref = O.dequant_gptq(qw, scales.astype(np.float32), qz, g, K, N, name, v1, wbits)
+        assert np.array_equal(got.float().numpy(), ref), (case, name)
+
+
+@pytest.mark.parametrize("G", [1, 4])
+def test_cpu_paths_rtn_and_gemm_match_oracle(G):
+    import torch
+
+    from oracle import cpu_paths as C
+
+    rng = np.random.default_rng(G)
+    K, N, M = 128, 40, 9
+    q = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    s = (np.abs(rng.standard_normal((N, G))) * 0.05 + 1e-3).astype(np.float16)
+    z = rng.uniform(-2, 17, (N, G)).astype(np.float16)
+    for dt, name in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        got = C.rtn_dequant(torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(z), K, dt)
+        ref = O.rtn_dequant(q, s.astype(np.float32), z.astype(np.float32), K, N, name)
+        assert np.array_equal(got.float().numpy(), ref)
+        x = torch.randn(M, K, generator=torch.Generator().manual_seed(G)).to(dt)
+        lin = C.PackedRTN(torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(z), K, dt)
+        ok, rel, cos = O.gemm_close(lin(x).float().numpy(), O.rtn_linear(x.float().numpy(), q, s.astype(np.float32),
+                                                                         z.astype(np.float32), K, N, name))
+        assert ok and torch.equal(lin.eager()(x), lin(x)), (rel, cos)
+    ids = torch.from_numpy(rng.integers(0, N, 17))
+    emb = C.embedding(ids, torch.from_numpy(q), torch.from_numpy(s), torch.from_numpy(z), K)
+    assert emb.dtype == torch.float16
+    assert np.array_equal(emb.float().numpy(), O.embedding(ids.numpy(), q, s.astype(np.float32),
+                                                           z.astype(np.float32), K, "f16"))
+
+
+def test_cpu_paths_gptq_linear_matches_oracle():
+    import torch
+
+    from oracle import cpu_paths as C
+
+    rng = np.random.default_rng(11)
+    K, N, M = 256, 64, 7
+    codes, zeros = rng.integers(0, 16, (K, N)), rng.integers(0, 16, (K // 32, N))
+    scales = (np.abs(rng.standard_normal((K // 32, N))) * 0.01 + 1e-3).astype(np.float16)
+    g = rng.permutation(K) // 32
+    qw, qz = O.pack_rows(codes), O.pack_zeros(zeros, True)
+    bias = rng.standard_normal(N).astype(np.float32)
+    x = torch.randn(M, K, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    lin = C.PackedGPTQ(torch.from_numpy(qw), torch.from_numpy(scales), torch.from_numpy(qz), torch.from_numpy(g),
+                       K, N, torch.bfloat16, True, torch.from_numpy(bias))
+    ref = O.gptq_linear(x.float().numpy(), qw, scales.astype(np.float32), qz, g, K, N, "bf16", True, bias=bias)
+    ok, rel, cos = O.gemm_close(lin(x).float().numpy(), ref)
+    assert ok, (rel, cos)
+    assert torch.equal(lin.eager()(x), lin(x))
