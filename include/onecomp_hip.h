@@ -116,6 +116,60 @@ int oc_int4_prepare(const int32_t *qweight, int32_t K, int32_t N,
                     void *st, int32_t *zt, void *stream);
 
 /*
+ * Device, load time: the 8-bit counterpart of oc_int4_prepare (GPTQ wbits=8:
+ * 4 codes per int32 word, mask 0xFF, quant_utils.py:21-22). Same arguments;
+ * inputs qweight [ceil(K/4), N], qzeros [>= G, N/4] (v1 restores
+ * (z + 1) & 0xFF); N % 4 == 0. Output layout ("tile16x8"):
+ *   qt  int32 [tiles][K_phys/32][16][8]   word (t, ks, c, w) = the codes of
+ *        physical rows 32ks + 4w .. +3 (byte i = row 4w + i) of column 16t + c
+ *   st  16-bit [tiles][G][16]            as in the 4-bit layout
+ *   zt  int32 [tiles][G][4]              4 zero bytes per word (columns
+ *        16t + 4h .. +3), stored as the zero itself
+ */
+int oc_int8_prepare(const int32_t *qweight, int32_t K, int32_t N,
+                    const int32_t *kmap, int32_t K_phys, int32_t group_rows,
+                    const void *scales, int32_t scale_dtype,
+                    const int32_t *qzeros, int32_t zero_mode, int32_t *qt,
+                    void *st, int32_t *zt, void *stream);
+
+/*
+ * Device: fused 8-bit GPTQ dequant + GEMM over the oc_int8_prepare layout,
+ * C = A' @ Wd + bias with Wd = RNE_a(f32(scale) * (code - zero)) exactly as
+ * dequant_gptq_to_fp (quant_utils.py:50-69) and fp32 accumulation; the
+ * fused counterpart of PackedGPTQLinear.forward for wbits = 8
+ * (layers/packed_gptq_linear.py:66-74), which dequantizes the whole weight
+ * per call. Arguments and workspace as oc_int4_gemm (one LDS-tiled MFMA
+ * kernel at every M; K split over fp32 partials when the grid is small;
+ * act-order rows gathered into the workspace). N % 4 == 0.
+ */
+int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M,
+                 int32_t K_logical, const int32_t *qt, const void *st,
+                 int32_t scale_dtype, const int32_t *zt, int32_t N,
+                 int32_t K_phys, int32_t group_rows, const int32_t *kmap,
+                 const uint16_t *kinv, const void *bias, int32_t bias_dtype,
+                 void *c, int64_t ldc, void *workspace, size_t workspace_bytes,
+                 void *stream);
+
+/* Workspace bytes oc_int8_gemm needs for this call shape (0 if none). */
+size_t oc_int8_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys,
+                                    int32_t group_rows, int32_t has_kmap);
+
+/* Device: the 8-bit counterpart of oc_int4_export (qweight
+ * [ceil(out_rows/4), N], qzeros [out_groups, N/4]; v1 stores zero - 1 mod 256). */
+int oc_int8_export(const int32_t *qt, const void *st, const int32_t *zt,
+                   int32_t N, int32_t K_phys, int32_t group_rows,
+                   const int32_t *row_src, int32_t out_rows,
+                   int32_t out_groups, int32_t zero_mode, int32_t *qweight,
+                   void *scales, int32_t *qzeros, void *stream);
+
+/* Device: the 8-bit counterpart of oc_int4_dequant_tiled. */
+int oc_int8_dequant_tiled(const int32_t *qt, const void *st,
+                          int32_t scale_dtype, const int32_t *zt,
+                          const int32_t *kmap, int32_t N, int32_t K_phys,
+                          int32_t group_rows, int32_t K_logical, void *out,
+                          int32_t out_dtype, void *stream);
+
+/*
  * Device, checkpoint export (state_dict): the inverse of oc_int4_prepare.
  * Writes the layer back in the checkpoint formats of the header comment, in
  * the buffer layout the reference's modules register:

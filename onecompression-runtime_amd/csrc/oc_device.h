@@ -137,6 +137,21 @@ __device__ __forceinline__ uint4 dequant8(uint32_t q, GroupParam gp) {
   return uint4{lo.x, hi.x, lo.y, hi.y};
 }
 
+// 8-bit GPTQ codes: the 8 codes of two words (code i = byte i % 4 of word
+// i / 4), each RNE_DT(s * (code - zero)). With c = -s * zero exact, fma(code,
+// s, c) is the exact product s * (code - zero) (a 16-bit scale times an
+// integer of at most 9 bits fits fp32), rounded once on packing.
+template <int DT>
+__device__ __forceinline__ uint4 dequant8_u8(uint32_t q0, uint32_t q1, float s, float c) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[i] = __builtin_fmaf(static_cast<float>((q0 >> (8 * i)) & 0xFFu), s, c);
+    f[4 + i] = __builtin_fmaf(static_cast<float>((q1 >> (8 * i)) & 0xFFu), s, c);
+  }
+  return uint4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
+}
+
 // ---- tiled GPTQ layout ("tile16") ---------------------------------------------
 //
 // Built once per layer by oc_int4_prepare. Output features are cut into tiles
@@ -149,6 +164,10 @@ __device__ __forceinline__ uint4 dequant8(uint32_t q, GroupParam gp) {
 //   zero word(t, g, h)  zt[(t * G + g) * 2 + h]   (columns 8h..8h+7, stored
 //                                                   as the zero itself)
 // KS = K_phys / 32 and G = K_phys / group_rows; columns past N are zero.
+// 8-bit layers use the same tiles with 8 words per column and K step (rows
+// 4w..4w+3 of the step in word w, one byte each) and 4 zero bytes per word:
+//   word8(t, ks, c, w)  qt[((t * KS + ks) * 16 + c) * 8 + w]
+//   zero word8(t, g, h) zt[(t * G + g) * 4 + h]   (columns 4h..4h+3)
 constexpr int TILE_N = 16;
 
 __device__ __forceinline__ int tile_zero(uint32_t zword, int c) {

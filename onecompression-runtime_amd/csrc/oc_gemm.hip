@@ -503,6 +503,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   // compile-time stage numbers stay in registers.
   uint32_t sa[PF][A_PER_THREAD * 4];
   uint32_t sq[PF][WN], ss[PF][WN], sz[PF][WN];
+  uint32_t sq8[PF][WN];  // 8-bit: the second word of the lane's 8 codes
   auto load = [&](auto fc, int ks) __attribute__((always_inline)) {
     constexpr int f = decltype(fc)::value;
     ks = min(ks, max(ks_end - 1, 0));
@@ -517,6 +518,18 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int tl = min(tw + j, last_tile);
+      if constexpr (FMT == FMT_GPTQ8) {
+        // Codes of K rows 8 quad .. 8 quad + 7: words 2 quad, 2 quad + 1.
+        const uint2 v = *reinterpret_cast<const uint2 *>(
+            static_cast<const uint32_t *>(p.qw) + ((static_cast<int64_t>(tl) * p.KS + ks) * TILE_N + c16) * 8 +
+            2 * quad);
+        sq[f][j] = v.x;
+        sq8[f][j] = v.y;
+        const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
+        ss[f][j] = static_cast<const uint16_t *>(p.scales)[tgs * TILE_N + c16];
+        sz[f][j] = static_cast<const uint32_t *>(p.zeros)[tgs * 4 + (c16 >> 2)];
+        continue;
+      }
       sq[f][j] = load_word<FMT>(p, p.qw, tl, ks, quad, c16);
       if constexpr (FMT == FMT_GPTQ) {
         const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
@@ -569,6 +582,10 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
         for (int j = 0; j < WN; ++j) {
           if constexpr (FMT == FMT_GPTQ) {
             b[j] = dequant8<DT>(sq[f][j], make_group_param(scale_f32<SDT>(ss[f][j]), tile_zero(sz[f][j], c16)));
+          } else if constexpr (FMT == FMT_GPTQ8) {
+            const float sv = scale_f32<SDT>(ss[f][j]);
+            const float zv = static_cast<float>((sz[f][j] >> (8 * (c16 & 3))) & 0xFFu);
+            b[j] = dequant8_u8<DT>(sq[f][j], sq8[f][j], sv, -sv * zv);
           } else {
             RtnParam rp;
             if constexpr (RDT != 0) {
@@ -1378,11 +1395,114 @@ void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
   else launch_tiled<DT, SDT, FMT_GPTQ>(p, sp.tile, s);
 }
 
+// 8-bit layers run the LDS-tiled kernel at every M: the largest tile shape
+// whose grid fills the chip, K split over fp32 partials when even 64 x 64
+// tiles leave it short (act-order rows gathered into the workspace first).
+Plan plan_gemm8(int M, int N, int K_phys, bool has_kmap) {
+  Plan sp{};
+  sp.regime = OC_REGIME_TILED;
+  const int ksteps = K_phys / 32;
+  static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
+  static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
+  TileCfg pick = cfgs[2];
+  for (const TileCfg &c : cfgs) {
+    if (static_cast<int64_t>((M + 16 * c.wm - 1) / (16 * c.wm)) * ((N + 64 * c.wn - 1) / (64 * c.wn)) >= want) {
+      pick = c;
+      break;
+    }
+  }
+  sp.tile = pick;
+  const int tiles = ((M + 16 * pick.wm - 1) / (16 * pick.wm)) * ((N + 64 * pick.wn - 1) / (64 * pick.wn));
+  int ksplit = 1;
+  if (tiles < want) ksplit = std::min((want + tiles - 1) / tiles, std::max(1, ksteps / 8));
+  sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
+  sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
+  sp.gather = has_kmap;
+  return sp;
+}
+
 }  // namespace oc
 
 using namespace oc;
 
 extern "C" {
+
+size_t oc_int8_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap) {
+  if (M <= 0 || N <= 0 || K_phys <= 0 || group_rows <= 0) return 0;
+  return workspace_bytes(plan_gemm8(M, N, K_phys, has_kmap != 0), M, N, K_phys);
+}
+
+int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
+                 const void *st, int32_t scale_dtype, const int32_t *zt, int32_t N, int32_t K_phys,
+                 int32_t group_rows, const int32_t *kmap, const uint16_t *kinv, const void *bias,
+                 int32_t bias_dtype, void *c, int64_t ldc, void *workspace, size_t workspace_bytes_given,
+                 void *stream) {
+  clear_error();
+  if (M < 0 || N <= 0 || K_phys <= 0 || K_logical <= 0)
+    return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K_logical=%d K_phys=%d", M, N, K_logical, K_phys);
+  if (M == 0) return OC_OK;
+  if (!a || !qt || !st || !zt || !c) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!is_half_dtype(a_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "a_dtype must be F16 or BF16");
+  if (!is_half_dtype(scale_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "scale_dtype must be F16 or BF16");
+  if (bias && !is_float_dtype(bias_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "bad bias dtype");
+  if (N % 4 != 0) return fail(OC_ERR_SHAPE, "N must be a multiple of 4 (8-bit qzeros packing), got N=%d", N);
+  if (K_phys % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 || K_phys % group_rows != 0)
+    return fail(OC_ERR_SHAPE, "K_phys=%d / group_rows=%d must be multiples of 32 with K_phys %% group_rows == 0",
+                K_phys, group_rows);
+  if (!kmap && K_logical != K_phys)
+    return fail(OC_ERR_SHAPE, "K_logical=%d != K_phys=%d requires a kmap", K_logical, K_phys);
+  if (lda < K_logical || ldc < N) return fail(OC_ERR_SHAPE, "lda/ldc smaller than the row length");
+  if (lda % 8 != 0 || !aligned(a, 16))
+    return fail(OC_ERR_SHAPE, "activations need 16-byte aligned rows (lda %% 8 == 0)");
+  if (!aligned(qt, 16) || !aligned(kmap, 16) || !aligned(kinv, 16))
+    return fail(OC_ERR_SHAPE, "qweight, kmap and kinv must be 16-byte aligned");
+  const int64_t tiles = (N + TILE_N - 1) / TILE_N;
+  if (tiles * (K_phys / 32) * 512 >= (1LL << 31))
+    return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more");
+  const Plan sp = plan_gemm8(M, N, K_phys, kmap != nullptr);
+  const size_t need = workspace_bytes(sp, M, N, K_phys);
+  if (need > 0) {
+    if (!workspace || workspace_bytes_given < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                  workspace ? workspace_bytes_given : static_cast<size_t>(0));
+    if (!aligned(workspace, 256)) return fail(OC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  GemmParams p{};
+  p.a = a;
+  p.lda = lda;
+  p.M = M;
+  p.K_logical = K_logical;
+  p.qw = qt;
+  p.scales = st;
+  p.zeros = zt;
+  p.N = N;
+  p.K_phys = K_phys;
+  p.KS = K_phys / 32;
+  p.G = K_phys / group_rows;
+  p.group_rows = group_rows;
+  p.gshift = ilog2_exact(group_rows / 32);
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.c = c;
+  p.ldc = ldc;
+  p.ksplit = sp.ksplit;
+  p.ksteps_per_split = sp.ksteps_per_split;
+  char *ws_after_counters = need > 0 ? static_cast<char *>(workspace) + COUNTER_BYTES : nullptr;
+  if (sp.gather) {
+    launch_gather_cols(a, lda, M, K_logical, kmap, kinv, K_phys, ws_after_counters, stream);
+    p.a = ws_after_counters;
+    p.lda = K_phys;
+  }
+  if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(ws_after_counters + gather_bytes(sp, M, K_phys));
+  const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
+  if (bf && sbf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
+  else if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);
+  else if (sbf) launch_tiled<OC_DTYPE_F16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
+  else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
 
 size_t oc_int4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap,
                                     int32_t regime) {

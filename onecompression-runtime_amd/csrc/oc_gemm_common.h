@@ -13,7 +13,9 @@
 
 namespace oc {
 
-enum { FMT_GPTQ = 0, FMT_RTN = 1 };
+// Weight formats of the tiled GEMM: 4-bit GPTQ tile16, RTN uint8 nibbles
+// [N, K/2], 8-bit GPTQ tile16 (32 code bytes per column and K step).
+enum { FMT_GPTQ = 0, FMT_RTN = 1, FMT_GPTQ8 = 2 };
 
 struct GemmParams {
   const void *a;

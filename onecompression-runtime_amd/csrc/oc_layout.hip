@@ -102,6 +102,146 @@ __global__ __launch_bounds__(256) void dequant_tiled_kernel(const uint32_t *__re
   else static_cast<uint16_t *>(out)[o] = static_cast<uint16_t>(pack2<ODT>(v, 0.f));
 }
 
+// ---- 8-bit GPTQ (4 codes per int32, mask 0xFF) ----
+// One thread per tiled word (t, ks, c, w), w = 0..7: the codes of physical
+// rows 32 ks + 4 w + i (byte i) of column n = 16 t + c, from input rows kmap[.].
+__global__ __launch_bounds__(256) void prepare8_words_kernel(const int32_t *__restrict__ qin, int K, int N,
+                                                             const int32_t *__restrict__ kmap, int KS, int tiles,
+                                                             uint32_t *__restrict__ qt) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * KS * 128) return;
+  const int w = static_cast<int>(idx & 7);
+  const int c = static_cast<int>((idx >> 3) & 15);
+  const int64_t rest = idx >> 7;
+  const int ks = static_cast<int>(rest % KS);
+  const int t = static_cast<int>(rest / KS);
+  const int n = TILE_N * t + c;
+  uint32_t word = 0;
+  if (n < N) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int kp = 32 * ks + 4 * w + i;
+      const int src = kmap ? kmap[kp] : (kp < K ? kp : -1);
+      if (src >= 0 && src < K) {
+        const uint32_t v = static_cast<uint32_t>(qin[static_cast<int64_t>(src >> 2) * N + n]);
+        word |= ((v >> (8 * (src & 3))) & 0xFFu) << (8 * i);
+      }
+    }
+  }
+  qt[idx] = word;
+}
+
+// One thread per (t, g, c): scale copy; threads with c % 4 == 0 also write the
+// zero word of columns c..c+3, restored to the zero itself (v1 adds 1 mod 256).
+__global__ __launch_bounds__(256) void prepare8_meta_kernel(const uint16_t *__restrict__ scales,
+                                                            const int32_t *__restrict__ qzeros, int zero_mode,
+                                                            int N, int G, int tiles, uint16_t *__restrict__ st,
+                                                            uint32_t *__restrict__ zt) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * G * TILE_N) return;
+  const int c = static_cast<int>(idx & 15);
+  const int64_t tg = idx >> 4;
+  const int g = static_cast<int>(tg % G);
+  const int t = static_cast<int>(tg / G);
+  const int n = TILE_N * t + c;
+  st[idx] = n < N ? scales[static_cast<int64_t>(g) * N + n] : static_cast<uint16_t>(0);
+  if ((c & 3) == 0) {
+    uint32_t out = 0;
+    if (n < N) {
+      const uint32_t zw = static_cast<uint32_t>(qzeros[static_cast<int64_t>(g) * (N >> 2) + (n >> 2)]);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint32_t z = (zw >> (8 * j)) & 0xFFu;
+        if (zero_mode == OC_ZERO_V1) z = (z + 1) & 0xFFu;
+        if (n + j < N) out |= z << (8 * j);
+      }
+    }
+    zt[tg * 4 + (c >> 2)] = out;
+  }
+}
+
+// Dense [N, K_logical] weight of an 8-bit tiled layer (as dequant_tiled_kernel).
+template <int ODT>
+__global__ __launch_bounds__(256) void dequant8_tiled_kernel(const uint32_t *__restrict__ qt,
+                                                             const uint16_t *__restrict__ st, int scale_dtype,
+                                                             const uint32_t *__restrict__ zt,
+                                                             const int32_t *__restrict__ kmap, int N, int K_phys,
+                                                             int group_rows, int K_logical, void *__restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(N) * K_phys) return;
+  const int kp = static_cast<int>(idx % K_phys);
+  const int n = static_cast<int>(idx / K_phys);
+  const int k = kmap ? kmap[kp] : (kp < K_logical ? kp : -1);
+  if (k < 0 || k >= K_logical) return;
+  const int KS = K_phys / 32, G = K_phys / group_rows;
+  const int t = n / TILE_N, c = n % TILE_N;
+  const uint32_t word = qt[((static_cast<int64_t>(t) * KS + kp / 32) * TILE_N + c) * 8 + ((kp >> 2) & 7)];
+  const int code = static_cast<int>((word >> (8 * (kp & 3))) & 0xFFu);
+  const int64_t tg = static_cast<int64_t>(t) * G + kp / group_rows;
+  const uint16_t sb = st[tg * TILE_N + c];
+  const float sv = scale_dtype == OC_DTYPE_BF16 ? bf16_to_f32(sb) : f16_to_f32(sb);
+  const int z = static_cast<int>((zt[tg * 4 + (c >> 2)] >> (8 * (c & 3))) & 0xFFu);
+  const float v = sv * static_cast<float>(code - z);
+  const int64_t o = static_cast<int64_t>(n) * K_logical + k;
+  if constexpr (ODT == OC_DTYPE_F32) static_cast<float *>(out)[o] = v;
+  else static_cast<uint16_t *>(out)[o] = static_cast<uint16_t>(pack2<ODT>(v, 0.f));
+}
+
+// Checkpoint-format 8-bit words: qweight [ceil(out_rows / 4), N], code row
+// k = physical row row_src[k] (or k); zeros / past-K rows give zero codes.
+__global__ __launch_bounds__(256) void export8_words_kernel(const uint32_t *__restrict__ qt, int KS,
+                                                            const int32_t *__restrict__ row_src, int out_rows, int N,
+                                                            uint32_t *__restrict__ qweight) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int rows4 = (out_rows + 3) / 4;
+  if (idx >= static_cast<int64_t>(rows4) * N) return;
+  const int n = static_cast<int>(idx % N);
+  const int r = static_cast<int>(idx / N);
+  const int t = n / TILE_N, c = n % TILE_N;
+  const int K_phys = 32 * KS;
+  uint32_t word = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int k = 4 * r + i;
+    if (k >= out_rows) break;
+    const int kp = row_src ? row_src[k] : k;
+    if (kp < 0 || kp >= K_phys) continue;
+    const uint32_t w = qt[((static_cast<int64_t>(t) * KS + kp / 32) * TILE_N + c) * 8 + ((kp >> 2) & 7)];
+    word |= ((w >> (8 * (kp & 3))) & 0xFFu) << (8 * i);
+  }
+  qweight[idx] = word;
+}
+
+// One thread per 8-bit qzeros word (g, n / 4) and its 4 scales.
+__global__ __launch_bounds__(256) void export8_meta_kernel(const uint16_t *__restrict__ st,
+                                                           const uint32_t *__restrict__ zt, int G, int out_groups,
+                                                           int N, int zero_mode, uint16_t *__restrict__ scales,
+                                                           uint32_t *__restrict__ qzeros) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int words = N / 4;
+  if (idx >= static_cast<int64_t>(out_groups) * words) return;
+  const int g = static_cast<int>(idx / words);
+  const int n0 = 4 * static_cast<int>(idx % words);
+  const int t = n0 / TILE_N, c0 = n0 % TILE_N;
+  uint32_t zout = 0;
+  uint16_t sv[4] = {0, 0, 0, 0};
+  if (g < G) {
+    const int64_t tg = static_cast<int64_t>(t) * G + g;
+    const uint32_t zw = zt[tg * 4 + (c0 >> 2)];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t z = (zw >> (8 * j)) & 0xFFu;
+      if (zero_mode == OC_ZERO_V1) z = (z + 255u) & 0xFFu;
+      zout |= z << (8 * j);
+      sv[j] = st[tg * TILE_N + c0 + j];
+    }
+  }
+  qzeros[idx] = zout;
+  uint16_t *srow = scales + static_cast<int64_t>(g) * N + n0;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) srow[j] = sv[j];
+}
+
 // Checkpoint-format words from the tiled layout (the inverse of
 // prepare_words_kernel). One thread per output word (r, n) of
 // qweight [ceil(out_rows / 8), N]: code row k = 8r + i is physical row
@@ -291,6 +431,79 @@ int oc_int4_export(const int32_t *qt, const void *st, const int32_t *zt, int32_t
   hipLaunchKernelGGL(export_meta_kernel, dim3(grid_of(metas)), dim3(256), 0, s, static_cast<const uint16_t *>(st),
                      reinterpret_cast<const uint32_t *>(zt), K_phys / group_rows, out_groups, N, zero_mode,
                      static_cast<uint16_t *>(scales), reinterpret_cast<uint32_t *>(qzeros));
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_int8_prepare(const int32_t *qweight, int32_t K, int32_t N, const int32_t *kmap, int32_t K_phys,
+                    int32_t group_rows, const void *scales, int32_t scale_dtype, const int32_t *qzeros,
+                    int32_t zero_mode, int32_t *qt, void *st, int32_t *zt, void *stream) {
+  clear_error();
+  if (!qweight || !scales || !qzeros || !qt || !st || !zt) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!is_half_dtype(scale_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "scale_dtype must be F16 or BF16");
+  if (zero_mode != OC_ZERO_V1 && zero_mode != OC_ZERO_V2)
+    return fail(OC_ERR_INVALID_ARGUMENT, "zero_mode must be OC_ZERO_V1 or OC_ZERO_V2");
+  if (K <= 0 || N <= 0 || N % 4 != 0 || K_phys <= 0 || K_phys % 32 != 0 || group_rows <= 0 ||
+      group_rows % 32 != 0 || K_phys % group_rows != 0)
+    return fail(OC_ERR_SHAPE, "bad shape K=%d N=%d K_phys=%d group_rows=%d", K, N, K_phys, group_rows);
+  const int tiles = (N + TILE_N - 1) / TILE_N;
+  const int KS = K_phys / 32, G = K_phys / group_rows;
+  if (static_cast<int64_t>(tiles) * KS * 512 >= (1LL << 31))
+    return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more (K_phys=%d N=%d)", K_phys, N);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t words = static_cast<int64_t>(tiles) * KS * 128;
+  hipLaunchKernelGGL(prepare8_words_kernel, dim3(grid_of(words)), dim3(256), 0, s, qweight, K, N, kmap, KS, tiles,
+                     reinterpret_cast<uint32_t *>(qt));
+  const int64_t metas = static_cast<int64_t>(tiles) * G * TILE_N;
+  hipLaunchKernelGGL(prepare8_meta_kernel, dim3(grid_of(metas)), dim3(256), 0, s,
+                     static_cast<const uint16_t *>(scales), qzeros, zero_mode, N, G, tiles,
+                     static_cast<uint16_t *>(st), reinterpret_cast<uint32_t *>(zt));
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_int8_export(const int32_t *qt, const void *st, const int32_t *zt, int32_t N, int32_t K_phys,
+                   int32_t group_rows, const int32_t *row_src, int32_t out_rows, int32_t out_groups,
+                   int32_t zero_mode, int32_t *qweight, void *scales, int32_t *qzeros, void *stream) {
+  clear_error();
+  if (!qt || !st || !zt || !qweight || !scales || !qzeros) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (zero_mode != OC_ZERO_V1 && zero_mode != OC_ZERO_V2)
+    return fail(OC_ERR_INVALID_ARGUMENT, "zero_mode must be OC_ZERO_V1 or OC_ZERO_V2");
+  if (N <= 0 || N % 4 != 0 || K_phys <= 0 || K_phys % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 ||
+      K_phys % group_rows != 0 || out_rows <= 0 || out_groups <= 0)
+    return fail(OC_ERR_SHAPE, "bad shape N=%d K_phys=%d group_rows=%d out_rows=%d out_groups=%d", N, K_phys,
+                group_rows, out_rows, out_groups);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t words = static_cast<int64_t>((out_rows + 3) / 4) * N;
+  hipLaunchKernelGGL(export8_words_kernel, dim3(grid_of(words)), dim3(256), 0, s,
+                     reinterpret_cast<const uint32_t *>(qt), K_phys / 32, row_src, out_rows, N,
+                     reinterpret_cast<uint32_t *>(qweight));
+  const int64_t metas = static_cast<int64_t>(out_groups) * (N / 4);
+  hipLaunchKernelGGL(export8_meta_kernel, dim3(grid_of(metas)), dim3(256), 0, s, static_cast<const uint16_t *>(st),
+                     reinterpret_cast<const uint32_t *>(zt), K_phys / group_rows, out_groups, N, zero_mode,
+                     static_cast<uint16_t *>(scales), reinterpret_cast<uint32_t *>(qzeros));
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_int8_dequant_tiled(const int32_t *qt, const void *st, int32_t scale_dtype, const int32_t *zt,
+                          const int32_t *kmap, int32_t N, int32_t K_phys, int32_t group_rows, int32_t K_logical,
+                          void *out, int32_t out_dtype, void *stream) {
+  clear_error();
+  if (!qt || !st || !zt || !out) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!is_half_dtype(scale_dtype) || !is_float_dtype(out_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "bad scale/out dtype");
+  if (N <= 0 || K_phys <= 0 || K_phys % 32 != 0 || group_rows <= 0 || group_rows % 32 != 0 ||
+      K_phys % group_rows != 0 || K_logical <= 0 || (!kmap && K_logical > K_phys))
+    return fail(OC_ERR_SHAPE, "bad shape N=%d K_phys=%d group_rows=%d K_logical=%d", N, K_phys, group_rows,
+                K_logical);
+  const int64_t total = static_cast<int64_t>(N) * K_phys;
+  auto kern = out_dtype == OC_DTYPE_BF16   ? dequant8_tiled_kernel<OC_DTYPE_BF16>
+              : out_dtype == OC_DTYPE_F16 ? dequant8_tiled_kernel<OC_DTYPE_F16>
+                                          : dequant8_tiled_kernel<OC_DTYPE_F32>;
+  hipLaunchKernelGGL(kern, dim3(grid_of(total)), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     reinterpret_cast<const uint32_t *>(qt), static_cast<const uint16_t *>(st), scale_dtype,
+                     reinterpret_cast<const uint32_t *>(zt), kmap, N, K_phys, group_rows, K_logical, out);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }

@@ -75,6 +75,24 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _P, _P, _I32, _I32, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P],
     ),
+    "oc_int8_prepare": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _P, _P],
+    ),
+    "oc_int8_gemm": (
+        ctypes.c_int,
+        [_P, _I64, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _I32,
+         _P, _I64, _P, _SZ, _P],
+    ),
+    "oc_int8_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
+    "oc_int8_export": (
+        ctypes.c_int,
+        [_P, _P, _P, _I32, _I32, _I32, _P, _I32, _I32, _I32, _P, _P, _P, _P],
+    ),
+    "oc_int8_dequant_tiled": (
+        ctypes.c_int,
+        [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _P, _I32, _P],
+    ),
     "oc_int4_dequant_tiled": (
         ctypes.c_int,
         [_P, _P, _I32, _P, _P, _I32, _I32, _I32, _I32, _P, _I32, _P],
@@ -243,6 +261,14 @@ def gemm_workspace_bytes(M: int, N: int, K_phys: int, group_rows: int, has_kmap:
 
 
 def gemm_workspace(device: torch.device | int, M: int, N: int, K_phys: int, group_rows: int,
-                   has_kmap: bool, regime: int, stream: int | None = None):
-    nbytes = gemm_workspace_bytes(M, N, K_phys, group_rows, has_kmap, regime)
+                   has_kmap: bool, regime: int, stream: int | None = None, wbits: int = 4):
+    if wbits == 8:
+        nbytes = gemm8_workspace_bytes(M, N, K_phys, group_rows, has_kmap)
+    else:
+        nbytes = gemm_workspace_bytes(M, N, K_phys, group_rows, has_kmap, regime)
     return workspace.get(device, nbytes, stream), nbytes
+
+
+@functools.lru_cache(maxsize=4096)
+def gemm8_workspace_bytes(M: int, N: int, K_phys: int, group_rows: int, has_kmap: bool) -> int:
+    return int(lib().oc_int8_gemm_workspace_bytes(M, N, K_phys, group_rows, int(has_kmap)))

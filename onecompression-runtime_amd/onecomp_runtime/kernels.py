@@ -78,19 +78,24 @@ def row_maps(plan: GroupPlan, device) -> tuple[torch.Tensor | None, torch.Tensor
 class TiledWeights:
     """A GPTQ layer in the tiled device layout of ``oc_int4_prepare``."""
 
-    qt: torch.Tensor  # int32 [tiles, K_phys/32, 16, 4]
+    qt: torch.Tensor  # int32 [tiles, K_phys/32, 16, 4] (8-bit: [..., 8])
     st: torch.Tensor  # fp16/bf16 [tiles, G, 16]
-    zt: torch.Tensor  # int32 [tiles, G, 2]
+    zt: torch.Tensor  # int32 [tiles, G, 2] (8-bit: [tiles, G, 4])
     N: int
     k_phys: int
     group_rows: int
+    wbits: int = 4
 
 
 def prepare(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, *, in_features: int,
             out_features: int, kmap: torch.Tensor | None, k_phys: int, group_rows: int,
-            v1: bool) -> TiledWeights:
+            v1: bool, wbits: int = 4) -> TiledWeights:
     """Build the tiled layout on the device (load time): rows permuted by
-    ``kmap`` into uniform groups, zeros restored to their value."""
+    ``kmap`` into uniform groups, zeros restored to their value. ``wbits``
+    4 (``oc_int4_prepare``) or 8 (``oc_int8_prepare``)."""
+    if wbits not in (4, 8):
+        raise ValueError(f"wbits must be 4 or 8, got {wbits}")
+    per = 32 // wbits
     dev = require_device(qweight, scales, qzeros, kmap)
     if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
         raise ValueError("qweight and qzeros must be int32")
@@ -100,25 +105,25 @@ def prepare(qweight: torch.Tensor, scales: torch.Tensor, qzeros: torch.Tensor, *
     N = int(out_features)
     tiles = (N + 15) // 16
     G = k_phys // group_rows
-    if qweight.dim() != 2 or qweight.shape[1] != N or qweight.shape[0] < (int(in_features) + 7) // 8:
+    if qweight.dim() != 2 or qweight.shape[1] != N or qweight.shape[0] < (int(in_features) + per - 1) // per:
         raise ValueError(f"qweight shape {tuple(qweight.shape)} does not hold {in_features} x {N} codes")
     if scales.dim() != 2 or scales.shape[1] != N or scales.shape[0] < G:
         raise ValueError(f"scales shape {tuple(scales.shape)} does not cover {G} groups x {N}")
-    if qzeros.dim() != 2 or qzeros.shape[1] != N // 8 or qzeros.shape[0] < G:
-        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover {G} groups x {N // 8}")
+    if qzeros.dim() != 2 or qzeros.shape[1] != N // per or qzeros.shape[0] < G:
+        raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover {G} groups x {N // per}")
     if kmap is not None and (kmap.dtype != torch.int32 or kmap.numel() != k_phys):
         raise ValueError(f"kmap must be int32 with {k_phys} entries")
-    qt = torch.empty((tiles, k_phys // 32, 16, 4), dtype=torch.int32, device=dev)
+    qt = torch.empty((tiles, k_phys // 32, 16, 4 if wbits == 4 else 8), dtype=torch.int32, device=dev)
     st = torch.empty((tiles, G, 16), dtype=scales.dtype, device=dev)
-    zt = torch.empty((tiles, G, 2), dtype=torch.int32, device=dev)
+    zt = torch.empty((tiles, G, 2 if wbits == 4 else 4), dtype=torch.int32, device=dev)
+    fn = lib().oc_int4_prepare if wbits == 4 else lib().oc_int8_prepare
     check(
-        lib().oc_int4_prepare(ptr(qweight), int(in_features), N, ptr(kmap), int(k_phys), int(group_rows),
-                              ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
-                              _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, ptr(qt), ptr(st), ptr(zt),
-                              stream_of(dev)),
-        "oc_int4_prepare",
+        fn(ptr(qweight), int(in_features), N, ptr(kmap), int(k_phys), int(group_rows),
+           ptr(scales), dtype_code(scales.dtype), ptr(qzeros),
+           _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2, ptr(qt), ptr(st), ptr(zt), stream_of(dev)),
+        f"oc_int{wbits}_prepare",
     )
-    return TiledWeights(qt, st, zt, N, int(k_phys), int(group_rows))
+    return TiledWeights(qt, st, zt, N, int(k_phys), int(group_rows), int(wbits))
 
 
 def export_checkpoint(w: TiledWeights, *, row_src: torch.Tensor | None, out_rows: int, out_groups: int,
@@ -132,14 +137,16 @@ def export_checkpoint(w: TiledWeights, *, row_src: torch.Tensor | None, out_rows
     if row_src is not None and (row_src.dtype != torch.int32 or row_src.numel() < out_rows):
         raise ValueError(f"row_src must be int32 with {out_rows} entries")
     N = w.N
-    qweight = torch.empty(((out_rows + 7) // 8, N), dtype=torch.int32, device=dev)
+    per = 32 // w.wbits
+    qweight = torch.empty(((out_rows + per - 1) // per, N), dtype=torch.int32, device=dev)
     scales = torch.empty((out_groups, N), dtype=w.st.dtype, device=dev)
-    qzeros = torch.empty((out_groups, N // 8), dtype=torch.int32, device=dev)
+    qzeros = torch.empty((out_groups, N // per), dtype=torch.int32, device=dev)
+    fn = lib().oc_int4_export if w.wbits == 4 else lib().oc_int8_export
     check(
-        lib().oc_int4_export(ptr(w.qt), ptr(w.st), ptr(w.zt), N, w.k_phys, w.group_rows, ptr(row_src),
-                             int(out_rows), int(out_groups), _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2,
-                             ptr(qweight), ptr(scales), ptr(qzeros), stream_of(dev)),
-        "oc_int4_export",
+        fn(ptr(w.qt), ptr(w.st), ptr(w.zt), N, w.k_phys, w.group_rows, ptr(row_src),
+           int(out_rows), int(out_groups), _hip.OC_ZERO_V1 if v1 else _hip.OC_ZERO_V2,
+           ptr(qweight), ptr(scales), ptr(qzeros), stream_of(dev)),
+        f"oc_int{w.wbits}_export",
     )
     return qweight, scales, qzeros
 
@@ -149,11 +156,11 @@ def dequant_tiled(w: TiledWeights, kmap: torch.Tensor | None, in_features: int,
     """Dense [N, in_features] weight (original K order) from the tiled layout."""
     dev = require_device(w.qt, kmap)
     out = torch.empty((w.N, int(in_features)), dtype=dtype, device=dev)
+    fn = lib().oc_int4_dequant_tiled if w.wbits == 4 else lib().oc_int8_dequant_tiled
     check(
-        lib().oc_int4_dequant_tiled(ptr(w.qt), ptr(w.st), dtype_code(w.st.dtype), ptr(w.zt), ptr(kmap), w.N,
-                                    w.k_phys, w.group_rows, int(in_features), ptr(out), dtype_code(dtype),
-                                    stream_of(dev)),
-        "oc_int4_dequant_tiled",
+        fn(ptr(w.qt), ptr(w.st), dtype_code(w.st.dtype), ptr(w.zt), ptr(kmap), w.N,
+           w.k_phys, w.group_rows, int(in_features), ptr(out), dtype_code(dtype), stream_of(dev)),
+        f"oc_int{w.wbits}_dequant_tiled",
     )
     return out
 
@@ -227,16 +234,21 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
     if out is None:
         out = torch.empty((M, N), dtype=adt, device=a_2d.device)
     stream = _hip._raw_stream(idx)
-    ws, nbytes = _hip.gemm_workspace(idx, M, N, w.k_phys, w.group_rows, kmap is not None, regime, stream)
-    status = _gemm_fn()(
+    ws, nbytes = _hip.gemm_workspace(idx, M, N, w.k_phys, w.group_rows, kmap is not None, regime, stream,
+                                     w.wbits)
+    args = (
         a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, in_features, qt.data_ptr(), w.st.data_ptr(),
         _DT[w.st.dtype], w.zt.data_ptr(), N, w.k_phys, w.group_rows,
         None if kmap is None else kmap.data_ptr(), None if kinv is None else kinv.data_ptr(),
         None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
-        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes, regime, stream,
+        out.data_ptr(), out.stride(0), None if ws is None else ws.data_ptr(), nbytes,
     )
+    if w.wbits == 4:
+        status = _gemm_fn()(*args, regime, stream)
+    else:
+        status = lib().oc_int8_gemm(*args, stream)
     if status:
-        check(status, "oc_int4_gemm")
+        check(status, f"oc_int{w.wbits}_gemm")
     return out
 
 

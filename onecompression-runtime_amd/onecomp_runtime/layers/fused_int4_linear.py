@@ -70,17 +70,20 @@ class _HipGPTQLinear(torch.nn.Module):
     """
 
     _STATE_LAYOUT = "input"
+    wbits = 4
 
     def _setup(self, in_features: int, out_features: int, qweight: torch.Tensor,
                scales: torch.Tensor, qzeros: torch.Tensor, bias: torch.Tensor | None,
-               groupsize: int, g_idx: torch.Tensor | None, v1: bool, kind: str) -> None:
+               groupsize: int, g_idx: torch.Tensor | None, v1: bool, kind: str, wbits: int = 4) -> None:
         self.in_features = int(in_features)
         self.out_features = int(out_features)
         self.groupsize = int(groupsize)
         self.v1 = bool(v1)
+        self.wbits = int(wbits)
         self._kind = kind
-        if self.out_features % 8 != 0:
-            raise ValueError(f"out_features must be a multiple of 8, got {self.out_features}")
+        per = 32 // self.wbits
+        if self.out_features % per != 0:
+            raise ValueError(f"out_features must be a multiple of {per}, got {self.out_features}")
         for name in ("qweight_tiled", "scales_tiled", "zeros_tiled", "kmap", "kinv",
                      "_src_qweight", "_src_scales", "_src_qzeros"):
             self.register_buffer(name, None, persistent=False)
@@ -112,16 +115,17 @@ class _HipGPTQLinear(torch.nn.Module):
             raise ValueError("qweight and qzeros must be int32")
         if qweight.dim() != 2 or qweight.shape[1] != self.out_features:
             raise ValueError(f"qweight has shape {tuple(qweight.shape)}, expected [*, {self.out_features}]")
-        rows_expected = (self.k_phys if physical else self.in_features + 7) // 8
+        per = 32 // self.wbits
+        rows_expected = (self.k_phys if physical else self.in_features + per - 1) // per
         if qweight.shape[0] < rows_expected:
             raise ValueError(f"qweight K-dim mismatch: got {qweight.shape[0]}, expected {rows_expected}")
         G = self.num_phys_groups
         if scales.dim() != 2 or scales.shape[0] < G or scales.shape[1] != self.out_features:
             raise ValueError(f"scales shape {tuple(scales.shape)} does not cover "
                              f"{G} groups x {self.out_features}")
-        if qzeros.dim() != 2 or tuple(qzeros.shape[1:]) != (self.out_features // 8,) or qzeros.shape[0] < G:
+        if qzeros.dim() != 2 or tuple(qzeros.shape[1:]) != (self.out_features // per,) or qzeros.shape[0] < G:
             raise ValueError(f"qzeros shape {tuple(qzeros.shape)} does not cover "
-                             f"{G} groups x {self.out_features // 8}")
+                             f"{G} groups x {self.out_features // per}")
 
     def _set_sources(self, qweight, scales, qzeros, *, physical: bool) -> None:
         """Checkpoint tensors (input row order, or ``physical`` row order) to be
@@ -142,11 +146,12 @@ class _HipGPTQLinear(torch.nn.Module):
         if self._src_physical:  # rows already in physical order: identity map
             w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
                                 in_features=self.k_phys, out_features=self.out_features, kmap=None,
-                                k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
+                                k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1, wbits=self.wbits)
         else:
             w = kernels.prepare(self._src_qweight, self._src_scales, self._src_qzeros,
                                 in_features=self.in_features, out_features=self.out_features,
-                                kmap=self.kmap, k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1)
+                                kmap=self.kmap, k_phys=self.k_phys, group_rows=self.group_rows, v1=self.v1,
+                                wbits=self.wbits)
         self.qweight_tiled, self.scales_tiled, self.zeros_tiled = w.qt, w.st, w.zt
         self._src_qweight = self._src_scales = self._src_qzeros = None
         self._weights = w
@@ -162,7 +167,7 @@ class _HipGPTQLinear(torch.nn.Module):
                         f"(its weights are on {self._src_qweight.device})")
                 return self._prepare()
             w = kernels.TiledWeights(self.qweight_tiled, self.scales_tiled, self.zeros_tiled,
-                                     self.out_features, self.k_phys, self.group_rows)
+                                     self.out_features, self.k_phys, self.group_rows, self.wbits)
             self._weights = w
         return w
 
@@ -174,7 +179,8 @@ class _HipGPTQLinear(torch.nn.Module):
             return k_pad, k_pad // self.groupsize
         if self._STATE_LAYOUT == "physical":
             return self.k_phys, max(self._ckpt_groups, self.num_phys_groups)
-        return max(8 * self._ckpt_rows, self.in_features), max(self._ckpt_groups, self.num_phys_groups)
+        return (max(32 // self.wbits * self._ckpt_rows, self.in_features),
+                max(self._ckpt_groups, self.num_phys_groups))
 
     def checkpoint_tensors(self) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """``(qweight, scales, qzeros)`` as the reference module holds them."""
@@ -337,7 +343,7 @@ class _HipGPTQLinear(torch.nn.Module):
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
-                f"groupsize={self.groupsize}, v1={self.v1}, k_phys={self.k_phys}, "
+                f"wbits={self.wbits}, groupsize={self.groupsize}, v1={self.v1}, k_phys={self.k_phys}, "
                 f"group_rows={self.group_rows}, backend=hip")
 
 

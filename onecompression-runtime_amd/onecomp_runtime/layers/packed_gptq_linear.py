@@ -11,9 +11,10 @@ materialised. The dequantized values are those of ``dequant_gptq_to_fp``
 summation order differs. The bias is rounded to ``x.dtype`` first, as the
 reference does (:73).
 
-fp32 activations and 8-bit layers keep the reference's two-step evaluation,
-on the device: a HIP dequant kernel writes the dense weight in ``x.dtype``
-and ``F.linear`` multiplies it.
+8-bit layers run the same way on their own tiled layout (``oc_int8_prepare``,
+``oc_int8_gemm``). fp32 activations keep the reference's two-step
+evaluation, on the device: a HIP dequant kernel writes the dense weight in
+``x.dtype`` and ``F.linear`` multiplies it.
 
 The module's state is the reference's: ``qweight``, ``scales``, ``qzeros``,
 ``g_idx`` (and ``bias``) as given.
@@ -54,23 +55,8 @@ class PackedGPTQLinear(_HipGPTQLinear):
         self._bias_cache: tuple | None = None
         # registered before the bias, as the reference does (state order)
         self.register_buffer("g_idx", g_idx.to(torch.long).contiguous())
-        if self.wbits == 4:
-            self._setup(in_features, out_features, qweight, scales, qzeros, bias, groupsize,
-                        g_idx, v1, "packed")
-        else:
-            self.in_features = int(in_features)
-            self.out_features = int(out_features)
-            self.groupsize = int(groupsize)
-            self.v1 = bool(v1)
-            self._kind = "packed"
-            self.kmap = None
-            self.register_buffer("_q8_qweight", qweight.contiguous(), persistent=False)
-            self.register_buffer("_q8_scales", scales.contiguous(), persistent=False)
-            self.register_buffer("_q8_qzeros", qzeros.contiguous(), persistent=False)
-            if bias is not None:
-                self.register_buffer("bias", bias.contiguous())
-            else:
-                self.bias = None
+        self._setup(in_features, out_features, qweight, scales, qzeros, bias, groupsize, g_idx, v1, "packed",
+                    wbits=self.wbits)
 
     def _bias_as(self, dtype: torch.dtype) -> torch.Tensor | None:
         """``bias.to(x.dtype)`` (packed_gptq_linear.py:73), cached per dtype."""
@@ -85,42 +71,11 @@ class PackedGPTQLinear(_HipGPTQLinear):
         return out
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.wbits == 4:
-            if x.dtype in (torch.float16, torch.bfloat16):
-                return self._gemm(x, bias=self._bias_as(x.dtype))
-            weight = self.dequantize(x.dtype)
-        else:
-            weight = kernels.int4_dequant(self._q8_qweight, self._q8_scales, self._q8_qzeros, self.g_idx,
-                                          self.in_features, self.out_features, x.dtype, v1=self.v1,
-                                          wbits=self.wbits)
-        return F.linear(x, weight, self._bias_as(x.dtype))
-
-    # 8-bit layers hold the checkpoint tensors themselves.
-    def checkpoint_tensors(self):
-        if self.wbits == 4:
-            return super().checkpoint_tensors()
-        return self._q8_qweight, self._q8_scales, self._q8_qzeros
-
-    def load_checkpoint(self, qweight, scales, qzeros, g_idx=None) -> None:
-        if self.wbits == 4:
-            return super().load_checkpoint(qweight, scales, qzeros, g_idx=g_idx)
-        dev = self._q8_qweight.device
-        self._q8_qweight = qweight.to(dev).contiguous()
-        self._q8_scales = scales.to(dev).contiguous()
-        self._q8_qzeros = qzeros.to(dev).contiguous()
-
-    def _apply(self, fn, recurse=True):
-        if self.wbits == 4:
-            return super()._apply(fn, recurse=recurse)
-        qw, qz, gi = self._q8_qweight, self._q8_qzeros, self.g_idx
-        result = torch.nn.Module._apply(self, fn, recurse=recurse)
-        if self._q8_qweight.dtype != torch.int32:
-            self._q8_qweight = qw.to(self._q8_qweight.device)
-        if self._q8_qzeros.dtype != torch.int32:
-            self._q8_qzeros = qz.to(self._q8_qzeros.device)
-        if self.g_idx.dtype != torch.long:
-            self.g_idx = gi.to(self.g_idx.device)
-        return result
+        if x.dtype in (torch.float16, torch.bfloat16):
+            return self._gemm(x, bias=self._bias_as(x.dtype))
+        # fp32 activations: the reference's evaluation, dequantize to x.dtype
+        # (exact fp32 products) then F.linear
+        return F.linear(x, self.dequantize(x.dtype), self._bias_as(x.dtype))
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
