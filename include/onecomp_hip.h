@@ -350,6 +350,46 @@ int oc_rtn_embedding(const int64_t *ids, int64_t T, const uint8_t *qweight_u8,
                      int32_t *bad_id_flag, void *stream);
 
 /*
+ * DeepSeek-V4 QEP packed layers (layers/dsv4_packed_linear.py:22-102):
+ *   qweight uint8 [N, row_bytes]: per = 8 / wbits codes per byte along the
+ *           in-dim, code(n, k) = (qweight[n][k / per] >> (wbits * (k % per)))
+ *           & (2^wbits - 1) (int4: the RTN nibble order; int2: 4 per byte)
+ *   scales / zeros of scale_dtype / zero_dtype in {F16, BF16, F32}, element
+ *           (n, g) at n * sz_stride_n + g * sz_stride_g (either orientation of
+ *           the reference's [G, N] / [N, G]); g = k / groupsize, or one per
+ *           row when groupsize <= 0
+ *   Wd[n, k] = RNE_out( fp32( fp32(code - zero) * scale ) )   (two fp32 ops)
+ */
+/* Device: dense out [N, K] (bit-exact with dequant_dsv4_packed; wbits 2, 4, 8). */
+int oc_dsv4_dequant(const uint8_t *qweight, int32_t N, int32_t row_bytes,
+                    int32_t wbits, int32_t K, const void *scales,
+                    int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
+                    int32_t groupsize, int64_t sz_stride_n, int64_t sz_stride_g,
+                    void *out, int32_t out_dtype, void *stream);
+
+/*
+ * Device: fused DSV4 dequant + GEMM, C[M, N] = X @ Wd^T + bias, Wd rounded to
+ * x_dtype as above (the reference dequantizes to x.dtype and calls F.linear,
+ * dsv4_packed_linear.py:94-98), fp32 accumulation, bias rounded to x_dtype by
+ * the caller. wbits in {2, 4}; K % 32 == 0; groupsize % 8 == 0 or <= 0;
+ * row_bytes >= K / per and a multiple of 4 (int4) or 2 (int2). LDS-tiled
+ * MFMA kernel at every M, K split over fp32 partials in the workspace
+ * (>= oc_dsv4_gemm_workspace_bytes, zero-filled counter area first) when
+ * the grid is small. The weights may sit in a staging buffer filled by an
+ * asynchronous host-to-device copy on another stream (expert offload).
+ */
+int oc_dsv4_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t M,
+                 int32_t K, const uint8_t *qweight, int32_t row_bytes,
+                 int32_t wbits, const void *scales, int32_t scale_dtype,
+                 const void *zeros, int32_t zero_dtype, int32_t groupsize,
+                 int64_t sz_stride_n, int64_t sz_stride_g, int32_t N,
+                 const void *bias, int32_t bias_dtype, void *c, int64_t ldc,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes oc_dsv4_gemm needs for this call shape (0 if none). */
+size_t oc_dsv4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K);
+
+/*
  * Device: MoE routing prologue (no reference counterpart: the reference has
  * no grouped GEMM; its MoE path loops over experts, layers/dsv4_packed_linear.py:95-98).
  * Stable counting sort of the T*topk (token, slot) pairs by expert id:

@@ -152,6 +152,29 @@ __device__ __forceinline__ uint4 dequant8_u8(uint32_t q0, uint32_t q1, float s, 
   return uint4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
 }
 
+// DSV4 codes (layers/dsv4_packed_linear.py:47-56): the 8 codes of q (code i
+// at bits BITS * i), each RNE_DT((f32(code) - z) * s) with the subtraction and
+// the product rounded in fp32 as the reference's torch ops do (two separate
+// fp32 operations, not a fused multiply-add).
+// The fp32 product passes through an empty asm (no instruction): folded into
+// the fp16 packing conversion (v_fma_mixlo_f16), it would be rounded once
+// instead of to fp32 first, and differ from the reference on fp16 ties.
+__device__ __forceinline__ float opaque(float v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}
+
+template <int DT, int BITS>
+__device__ __forceinline__ uint4 dsv4_dequant8(uint32_t q, float s, float z) {
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float d = __fsub_rn(static_cast<float>((q >> (BITS * i)) & ((1u << BITS) - 1)), z);
+    f[i] = opaque(__fmul_rn(d, s));
+  }
+  return uint4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
+}
+
 // ---- tiled GPTQ layout ("tile16") ---------------------------------------------
 //
 // Built once per layer by oc_int4_prepare. Output features are cut into tiles

@@ -405,8 +405,11 @@ __device__ __forceinline__ uint32_t load_word(const GemmParams &p, const void *q
     // Clamped like the RTN scale/zero rows: with N % 16 == 8 the upper lanes
     // of the last tile name rows past the weight (their results are unused).
     const int n = min(TILE_N * tile + c16, p.N - 1);
-    return *reinterpret_cast<const uint32_t *>(static_cast<const uint8_t *>(qw) +
-                                               static_cast<int64_t>(n) * p.row_bytes + 16 * ks + 4 * quad);
+    const uint8_t *row = static_cast<const uint8_t *>(qw) + static_cast<int64_t>(n) * p.row_bytes;
+    if constexpr (FMT == FMT_DSV4_2)  // 8 two-bit codes: 2 bytes
+      return *reinterpret_cast<const uint16_t *>(row + 8 * ks + 2 * quad);
+    else
+      return *reinterpret_cast<const uint32_t *>(row + 16 * ks + 4 * quad);
   }
 }
 
@@ -537,7 +540,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
         sz[f][j] = static_cast<const uint32_t *>(p.zeros)[tgs * 2 + (c16 >> 3)];
       } else {
         const int n = min(TILE_N * tl + c16, p.N - 1);
-        const int64_t i = static_cast<int64_t>(n) * p.rtn_G + (32 * ks + 8 * quad) / p.rtn_gs;
+        const int64_t i = static_cast<int64_t>(n) * p.sz_stride_n + ((32 * ks + 8 * quad) / p.rtn_gs) * p.sz_stride_g;
         if constexpr (RDT != 0) {
           ss[f][j] = static_cast<const uint16_t *>(p.scales)[i];
           sz[f][j] = static_cast<const uint16_t *>(p.zeros)[i];
@@ -586,6 +589,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
             const float sv = scale_f32<SDT>(ss[f][j]);
             const float zv = static_cast<float>((sz[f][j] >> (8 * (c16 & 3))) & 0xFFu);
             b[j] = dequant8_u8<DT>(sq[f][j], sq8[f][j], sv, -sv * zv);
+          } else if constexpr (FMT == FMT_DSV4_4 || FMT == FMT_DSV4_2) {
+            float sv, zv;
+            if constexpr (RDT != 0) {
+              sv = half_to_f32<RDT>(ss[f][j]);
+              zv = half_to_f32<RDT>(sz[f][j]);
+            } else {
+              sv = __uint_as_float(ss[f][j]);
+              zv = __uint_as_float(sz[f][j]);
+            }
+            b[j] = dsv4_dequant8<DT, FMT == FMT_DSV4_2 ? 2 : 4>(sq[f][j], sv, zv);
           } else {
             RtnParam rp;
             if constexpr (RDT != 0) {
@@ -1334,12 +1347,12 @@ void launch_mfma(const GemmParams &p, int mt, hipStream_t s) {
 template <int DT, int SDT, int WM, int WN, int FMT>
 void launch_tiled_t(const GemmParams &p, hipStream_t s) {
   const dim3 grid((p.N + 64 * WN - 1) / (64 * WN), (p.M + 16 * WM - 1) / (16 * WM), p.ksplit);
-  const bool same16 = FMT == FMT_RTN && p.scale_dtype == p.zero_dtype;
+  const bool same16 = fmt_rows(FMT) && p.scale_dtype == p.zero_dtype;
   if (same16 && p.scale_dtype == OC_DTYPE_F16)
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, FMT == FMT_RTN ? OC_DTYPE_F16 : 0>), grid, dim3(256), 0,
-                       s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_F16 : 0>), grid, dim3(256),
+                       0, s, p);
   else if (same16 && p.scale_dtype == OC_DTYPE_BF16)
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, FMT == FMT_RTN ? OC_DTYPE_BF16 : 0>), grid, dim3(256),
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_BF16 : 0>), grid, dim3(256),
                        0, s, p);
   else
     hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0>), grid, dim3(256), 0, s, p);
@@ -1395,10 +1408,10 @@ void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
   else launch_tiled<DT, SDT, FMT_GPTQ>(p, sp.tile, s);
 }
 
-// 8-bit layers run the LDS-tiled kernel at every M: the largest tile shape
+// 8-bit GPTQ and DSV4 layers run the LDS-tiled kernel at every M: the largest tile shape
 // whose grid fills the chip, K split over fp32 partials when even 64 x 64
 // tiles leave it short (act-order rows gathered into the workspace first).
-Plan plan_gemm8(int M, int N, int K_phys, bool has_kmap) {
+Plan plan_tiled_only(int M, int N, int K_phys, bool has_kmap) {
   Plan sp{};
   sp.regime = OC_REGIME_TILED;
   const int ksteps = K_phys / 32;
@@ -1429,7 +1442,7 @@ extern "C" {
 
 size_t oc_int8_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap) {
   if (M <= 0 || N <= 0 || K_phys <= 0 || group_rows <= 0) return 0;
-  return workspace_bytes(plan_gemm8(M, N, K_phys, has_kmap != 0), M, N, K_phys);
+  return workspace_bytes(plan_tiled_only(M, N, K_phys, has_kmap != 0), M, N, K_phys);
 }
 
 int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
@@ -1459,7 +1472,7 @@ int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   const int64_t tiles = (N + TILE_N - 1) / TILE_N;
   if (tiles * (K_phys / 32) * 512 >= (1LL << 31))
     return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more");
-  const Plan sp = plan_gemm8(M, N, K_phys, kmap != nullptr);
+  const Plan sp = plan_tiled_only(M, N, K_phys, kmap != nullptr);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
   if (need > 0) {
     if (!workspace || workspace_bytes_given < need)
@@ -1500,6 +1513,81 @@ int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   else if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);
   else if (sbf) launch_tiled<OC_DTYPE_F16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
   else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+size_t oc_dsv4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K) {
+  if (M <= 0 || N <= 0 || K <= 0 || K % 32 != 0) return 0;
+  return workspace_bytes(plan_tiled_only(M, N, K, false), M, N, K);
+}
+
+int oc_dsv4_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_t K, const uint8_t *qweight,
+                 int32_t row_bytes, int32_t wbits, const void *scales, int32_t scale_dtype, const void *zeros,
+                 int32_t zero_dtype, int32_t groupsize, int64_t sz_stride_n, int64_t sz_stride_g, int32_t N,
+                 const void *bias, int32_t bias_dtype, void *c, int64_t ldc, void *workspace,
+                 size_t workspace_bytes_given, void *stream) {
+  clear_error();
+  if (M < 0 || N <= 0 || K <= 0) return fail(OC_ERR_SHAPE, "bad shape M=%d N=%d K=%d", M, N, K);
+  if (M == 0) return OC_OK;
+  if (!x || !qweight || !scales || !zeros || !c) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (wbits != 2 && wbits != 4) return fail(OC_ERR_INVALID_ARGUMENT, "wbits must be 2 or 4, got %d", wbits);
+  if (!is_half_dtype(x_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "x_dtype must be F16 or BF16");
+  if (!is_float_dtype(scale_dtype) || !is_float_dtype(zero_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "scales and zeros must be F16, BF16 or F32");
+  if (bias && !is_float_dtype(bias_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "bad bias dtype");
+  const int per = 8 / wbits;
+  if (K % 32 != 0 || (groupsize > 0 && groupsize % 8 != 0) || row_bytes < K / per)
+    return fail(OC_ERR_UNSUPPORTED,
+                "fused DSV4 GEMM needs K %% 32 == 0, groupsize %% 8 == 0 (or per row) and rows of K / %d bytes "
+                "(K=%d groupsize=%d row_bytes=%d)", per, K, groupsize, row_bytes);
+  if (row_bytes % (wbits == 4 ? 4 : 2) != 0 || !aligned(qweight, 4))
+    return fail(OC_ERR_SHAPE, "qweight rows must be %d-byte aligned", wbits == 4 ? 4 : 2);
+  if (ldx % 8 != 0 || !aligned(x, 16) || ldx < K || ldc < N)
+    return fail(OC_ERR_SHAPE, "x needs 16-byte aligned rows (ldx %% 8 == 0)");
+  const Plan sp = plan_tiled_only(M, N, K, false);
+  const size_t need = workspace_bytes(sp, M, N, K);
+  if (need > 0) {
+    if (!workspace || workspace_bytes_given < need)
+      return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                  workspace ? workspace_bytes_given : static_cast<size_t>(0));
+    if (!aligned(workspace, 256)) return fail(OC_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  }
+  GemmParams p{};
+  p.a = x;
+  p.lda = ldx;
+  p.M = M;
+  p.K_logical = K;
+  p.qw = qweight;
+  p.scales = scales;
+  p.zeros = zeros;
+  p.scale_dtype = scale_dtype;
+  p.zero_dtype = zero_dtype;
+  p.rtn_gs = groupsize > 0 ? groupsize : K;  // per row: one group spanning K
+  p.row_bytes = row_bytes;
+  p.sz_stride_n = sz_stride_n;
+  p.sz_stride_g = groupsize > 0 ? sz_stride_g : 0;
+  p.N = N;
+  p.K_phys = K;
+  p.KS = K / 32;
+  p.group_rows = 32;
+  p.gshift = 0;
+  p.bias = bias;
+  p.bias_dtype = bias_dtype;
+  p.c = c;
+  p.ldc = ldc;
+  p.ksplit = sp.ksplit;
+  p.ksteps_per_split = sp.ksteps_per_split;
+  if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + COUNTER_BYTES);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool bf = x_dtype == OC_DTYPE_BF16;
+  if (wbits == 4) {
+    if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_DSV4_4>(p, sp.tile, s);
+    else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_DSV4_4>(p, sp.tile, s);
+  } else {
+    if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_DSV4_2>(p, sp.tile, s);
+    else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_DSV4_2>(p, sp.tile, s);
+  }
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
@@ -1668,6 +1756,8 @@ int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_
   p.rtn_G = G;
   p.rtn_gs = K / G;
   p.row_bytes = row_bytes;
+  p.sz_stride_n = G;
+  p.sz_stride_g = 1;
   p.N = N;
   p.K_phys = K;
   p.KS = K / 32;

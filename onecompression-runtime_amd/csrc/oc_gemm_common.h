@@ -15,7 +15,10 @@ namespace oc {
 
 // Weight formats of the tiled GEMM: 4-bit GPTQ tile16, RTN uint8 nibbles
 // [N, K/2], 8-bit GPTQ tile16 (32 code bytes per column and K step).
-enum { FMT_GPTQ = 0, FMT_RTN = 1, FMT_GPTQ8 = 2 };
+// DSV4: uint8 [N, K / per] codes along the in-dim (int4: the RTN nibble
+// order; int2: 4 codes per byte, low bits first), fp32 dequant (q - z) * s.
+enum { FMT_GPTQ = 0, FMT_RTN = 1, FMT_GPTQ8 = 2, FMT_DSV4_4 = 3, FMT_DSV4_2 = 4 };
+constexpr bool fmt_rows(int f) { return f == FMT_RTN || f == FMT_DSV4_4 || f == FMT_DSV4_2; }
 
 struct GemmParams {
   const void *a;
@@ -28,9 +31,11 @@ struct GemmParams {
   const void *zeros;   // GPTQ: tile16 zero words; RTN: [N, G] of zero_dtype
   int scale_dtype;     // RTN (runtime)
   int zero_dtype;      // RTN (runtime)
-  int rtn_gs;          // RTN: columns per group
+  int rtn_gs;          // RTN / DSV4: columns per group
   int rtn_G;           // RTN: groups per row
-  int row_bytes;       // RTN
+  int row_bytes;       // RTN / DSV4
+  int64_t sz_stride_n;  // RTN / DSV4: scale/zero element offset per output row ...
+  int64_t sz_stride_g;  // ... and per group
   int N;
   int K_phys;
   int KS;              // K_phys / 32

@@ -95,7 +95,8 @@ __global__ __launch_bounds__(256) void gptq_dequant_generic_kernel(
   int z = static_cast<int>((zw >> (wbits * (n % per_word))) & mask);
   if (zero_mode == OC_ZERO_V1) z = (z + 1) & static_cast<int>(mask);
   const float s = load_any_f32(scales, static_cast<int64_t>(g) * N + n, scale_dtype);
-  const float p = s * static_cast<float>(code - z);
+  // rounded to fp32 before the output conversion (fp32 scales: the product may round)
+  const float p = opaque(s * static_cast<float>(code - z));
   store_out<ODT>(out, idx, p);
 }
 
@@ -190,6 +191,27 @@ __global__ __launch_bounds__(256) void rtn_embedding_scalar_kernel(
     const uint32_t byte = q[id * row_bytes + col / 2];
     v = rtn_value<ODT>(static_cast<int>((byte >> (4 * (col & 1))) & 0xFu), p);
   }
+  store_out<ODT>(out, idx, v);
+}
+
+// DSV4 dequant (layers/dsv4_packed_linear.py:22-56): one thread per output
+// element, out[n, k] = RNE_out(fp32(fp32(code - z) * s)).
+template <int ODT>
+__global__ __launch_bounds__(256) void dsv4_dequant_kernel(const uint8_t *__restrict__ q, int N, int row_bytes,
+                                                           int wbits, int K, const void *scales, int sdt,
+                                                           const void *zeros, int zdt, int groupsize,
+                                                           int64_t stride_n, int64_t stride_g, void *out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(N) * K) return;
+  const int k = static_cast<int>(idx % K);
+  const int n = static_cast<int>(idx / K);
+  const int per = 8 / wbits;
+  const int code = (q[static_cast<int64_t>(n) * row_bytes + k / per] >> (wbits * (k % per))) & ((1 << wbits) - 1);
+  const int64_t gi = static_cast<int64_t>(n) * stride_n + (groupsize > 0 ? static_cast<int64_t>(k / groupsize) * stride_g : 0);
+  const float sv = load_any_f32(scales, gi, sdt);
+  const float zv = load_any_f32(zeros, gi, zdt);
+  // rounded to fp32 before the output conversion (see opaque())
+  const float v = opaque(__fmul_rn(__fsub_rn(static_cast<float>(code), zv), sv));
   store_out<ODT>(out, idx, v);
 }
 
@@ -344,6 +366,29 @@ int oc_rtn_dequant(const uint8_t *qweight_u8, int32_t rows, int32_t row_bytes, c
                                           : rtn_dequant_kernel<OC_DTYPE_F32>;
   hipLaunchKernelGGL(kern, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream),
                      qweight_u8, rows, row_bytes, scales, scale_dtype, zeros, zero_dtype, G, K, out);
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_dsv4_dequant(const uint8_t *qweight, int32_t N, int32_t row_bytes, int32_t wbits, int32_t K,
+                    const void *scales, int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
+                    int32_t groupsize, int64_t sz_stride_n, int64_t sz_stride_g, void *out, int32_t out_dtype,
+                    void *stream) {
+  clear_error();
+  if (!qweight || !scales || !zeros || !out) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (wbits != 2 && wbits != 4 && wbits != 8) return fail(OC_ERR_INVALID_ARGUMENT, "wbits must be 2, 4 or 8");
+  if (!is_float_dtype(scale_dtype) || !is_float_dtype(zero_dtype) || !is_float_dtype(out_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "unsupported dtype");
+  const int per = 8 / wbits;
+  if (N <= 0 || K <= 0 || row_bytes < (K + per - 1) / per)
+    return fail(OC_ERR_SHAPE, "bad shape N=%d K=%d row_bytes=%d", N, K, row_bytes);
+  const int64_t total = static_cast<int64_t>(N) * K;
+  auto kern = out_dtype == OC_DTYPE_BF16   ? dsv4_dequant_kernel<OC_DTYPE_BF16>
+              : out_dtype == OC_DTYPE_F16 ? dsv4_dequant_kernel<OC_DTYPE_F16>
+                                          : dsv4_dequant_kernel<OC_DTYPE_F32>;
+  hipLaunchKernelGGL(kern, dim3(grid_for(total)), dim3(256), 0, static_cast<hipStream_t>(stream), qweight, N,
+                     row_bytes, wbits, K, scales, scale_dtype, zeros, zero_dtype, groupsize, sz_stride_n,
+                     sz_stride_g, out);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }

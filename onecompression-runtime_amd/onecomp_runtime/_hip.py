@@ -127,6 +127,16 @@ SIGNATURES = {
         ctypes.c_int,
         [_P, _I64, _P, _I64, _I32, _P, _I32, _P, _I32, _I32, _I32, _P, _I32, _P, _P],
     ),
+    "oc_dsv4_dequant": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _I32, _I64, _I64, _P, _I32, _P],
+    ),
+    "oc_dsv4_gemm": (
+        ctypes.c_int,
+        [_P, _I64, _I32, _I32, _I32, _P, _I32, _I32, _P, _I32, _P, _I32, _I32, _I64, _I64, _I32,
+         _P, _I32, _P, _I64, _P, _SZ, _P],
+    ),
+    "oc_dsv4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
     "oc_moe_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
     "oc_int4_moe_gemm": (
         ctypes.c_int,

@@ -369,3 +369,52 @@ def int4_moe_gemm(x: torch.Tensor, topk: int, w: TiledWeights, expert_offsets: t
         "oc_int4_moe_gemm",
     )
     return y
+
+
+def _dsv4_strides(scales: torch.Tensor, out_features: int, in_features: int, groupsize: int):
+    """Element strides (per output row, per group) of a DSV4 scale/zero tensor,
+    whichever of the reference's orientations it has (dsv4_packed_linear.py:40-51)."""
+    if groupsize <= 0:
+        return 1, 0
+    G = (in_features + groupsize - 1) // groupsize
+    if tuple(scales.shape) == (out_features, G):
+        return G, 1
+    if tuple(scales.shape) == (G, out_features):
+        return 1, out_features
+    raise ValueError(f"scales shape {tuple(scales.shape)} is neither ({out_features}, {G}) nor ({G}, {out_features})")
+
+
+def dsv4_dequant(qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *, wbits: int,
+                 groupsize: int, in_features: int, dtype: torch.dtype) -> torch.Tensor:
+    """Dense [out, in] weight, bit-exact with dequant_dsv4_packed (oc_dsv4_dequant)."""
+    dev = require_device(qweight, scales, zeros)
+    qweight, scales, zeros = qweight.contiguous(), scales.contiguous(), zeros.contiguous()
+    N = qweight.shape[0]
+    sn, sg = _dsv4_strides(scales, N, in_features, groupsize)
+    out = torch.empty((N, int(in_features)), dtype=dtype, device=dev)
+    check(lib().oc_dsv4_dequant(ptr(qweight), N, qweight.shape[1], int(wbits), int(in_features), ptr(scales),
+                                dtype_code(scales.dtype), ptr(zeros), dtype_code(zeros.dtype), int(groupsize), sn,
+                                sg, ptr(out), dtype_code(dtype), stream_of(dev)), "oc_dsv4_dequant")
+    return out
+
+
+def dsv4_gemm(x_2d: torch.Tensor, qweight: torch.Tensor, scales: torch.Tensor, zeros: torch.Tensor, *,
+              wbits: int, groupsize: int, in_features: int, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """C[M, N] = x @ dequant_dsv4(W)^T + bias (oc_dsv4_gemm), fp16/bf16 x."""
+    dev = require_device(x_2d, qweight, scales, zeros, bias)
+    if x_2d.stride(-1) != 1 or x_2d.stride(0) % 8 or x_2d.data_ptr() % 16:
+        x_2d = x_2d.contiguous()
+    M, K = x_2d.shape
+    N = qweight.shape[0]
+    sn, sg = _dsv4_strides(scales, N, in_features, groupsize)
+    out = torch.empty((M, N), dtype=x_2d.dtype, device=dev)
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    stream = _hip._raw_stream(idx)
+    nbytes = int(lib().oc_dsv4_gemm_workspace_bytes(M, N, K))
+    ws = _hip.workspace.get(idx, nbytes, stream)
+    check(lib().oc_dsv4_gemm(ptr(x_2d), x_2d.stride(0), dtype_code(x_2d.dtype), M, int(in_features), ptr(qweight),
+                             qweight.shape[1], int(wbits), ptr(scales), dtype_code(scales.dtype), ptr(zeros),
+                             dtype_code(zeros.dtype), int(groupsize), sn, sg, N, ptr(bias),
+                             dtype_code(bias.dtype) if bias is not None else 0, ptr(out), out.stride(0), ptr(ws),
+                             nbytes, stream), "oc_dsv4_gemm")
+    return out

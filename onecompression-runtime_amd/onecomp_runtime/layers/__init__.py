@@ -6,6 +6,8 @@
 - :class:`FusedInt4LinearAnyGroup` - any groupsize.
 - :class:`PackedGPTQLinear` - any groupsize, act-order ``g_idx``, 4/8-bit.
 - :class:`PackedRTNLinear` / :class:`PackedEmbedding` - RTN uint8-nibble layers.
+- :class:`Dsv4PackedLinear` - DeepSeek-V4 QEP int4/int2 layers, host-resident
+  experts staged to the device per call.
 - :class:`GemLiteInt4Linear` / :func:`gemlite_available` - import-compatible
   names only (GemLite is never available on this build).
 """
@@ -17,6 +19,7 @@ from .fused_int4_linear import (
     FusedInt4LinearPaddedGroups,
     fused_int4_gemm,
 )
+from .dsv4_packed_linear import Dsv4PackedLinear, dequant_dsv4_packed, run_routed_experts
 from .gemlite_int4_linear import GemLiteInt4Linear, gemlite_available
 from .packed_gptq_linear import PackedGPTQLinear
 from .packed_linear import PackedEmbedding, PackedRTNLinear
@@ -31,4 +34,7 @@ __all__ = [
     "PackedGPTQLinear",
     "PackedRTNLinear",
     "PackedEmbedding",
+    "Dsv4PackedLinear",
+    "dequant_dsv4_packed",
+    "run_routed_experts",
 ]

@@ -48,8 +48,8 @@ def dequant_gptq_to_fp(
 ) -> torch.Tensor:
     """Dequantize a GPTQ Linear to (out, in) ``dtype`` (quant_utils.py:50-69).
 
-    Bit-exact with the reference: one exact fp32 product ``s * (w - z)``
-    rounded once to ``dtype``.
+    Bit-exact with the reference: the fp32 product ``s * (w - z)`` (exact for
+    16-bit scales) rounded to ``dtype``.
     """
     return kernels.int4_dequant(qweight, scales, qzeros, g_idx, in_features, out_features, dtype,
                                 v1=v1, wbits=wbits)

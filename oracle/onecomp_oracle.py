@@ -20,6 +20,9 @@ How each function is pinned (tests/test_oracle.py):
                                special cases (s=1, z=8), v1/v2 and g_idx identities
     rtn_dequant             -> torch's 16-bit elementwise ops applied in the
                                reference's order on adversarial inputs; nibble KATs
+    dsv4_unpack / dequant   -> exact-rational known answers (kats.json: byte
+                               order, fp32 sub and mul rounding, output rounding),
+                               pack/unpack round trip, orientation identity
     embedding               -> row gather identity + output-dtype rule
     linear / gptq_linear    -> float64 brute force on tiny shapes; act-order and
                                padded-groups invariances
@@ -205,6 +208,58 @@ def embedding(ids, qweight_u8, scales, zeros, embedding_dim: int, dtype: str) ->
     q = np.asarray(qweight_u8)[flat]
     return rtn_dequant(q, np.asarray(scales)[flat], np.asarray(zeros)[flat], embedding_dim,
                        flat.shape[0], dtype)
+
+
+# ---------------------------------------------------------------------------
+# DSV4 (DeepSeek-V4 QEP) uint8 packing along the in-dim
+def dsv4_unpack(qweight_packed, wbits: int, in_features: int) -> np.ndarray:
+    """dequant_dsv4_packed's unpack (layers/dsv4_packed_linear.py:28-35): byte
+    j of row n holds columns per*j + i at bits wbits*i, per = 8 // wbits;
+    cropped to in_features. -> int32 [out, in]."""
+    per = 8 // wbits
+    q = np.asarray(qweight_packed, dtype=np.uint8).astype(np.int32)
+    out_f, ncol = q.shape
+    codes = np.empty((out_f, ncol, per), dtype=np.int32)
+    for i in range(per):
+        codes[:, :, i] = (q >> (wbits * i)) & ((1 << wbits) - 1)
+    return codes.reshape(out_f, ncol * per)[:, :in_features]
+
+
+def dsv4_pack(codes, wbits: int) -> np.ndarray:
+    """Inverse of dsv4_unpack: int codes [out, in] -> uint8 [out, ceil(in / per)]."""
+    per = 8 // wbits
+    c = np.asarray(codes, dtype=np.int64)
+    out_f, k = c.shape
+    kp = (k + per - 1) // per * per
+    full = np.zeros((out_f, kp), dtype=np.int64)
+    full[:, :k] = c & ((1 << wbits) - 1)
+    full = full.reshape(out_f, kp // per, per)
+    b = np.zeros((out_f, kp // per), dtype=np.int64)
+    for i in range(per):
+        b |= full[:, :, i] << (wbits * i)
+    return b.astype(np.uint8)
+
+
+def dequant_dsv4(qweight_packed, scales, qzeros, wbits: int, groupsize: int, in_features: int,
+                 dtype: str) -> np.ndarray:
+    """dequant_dsv4_packed (layers/dsv4_packed_linear.py:22-56) -> [out, in]
+    float32 holding values of ``dtype``: in fp32, (q - z) then * s (each op
+    rounded), one rounding to ``dtype``. Scales / zeros [G, out] or [out, G]
+    (transposed when shaped (out, G), :49-50); groupsize <= 0: one per row."""
+    q = dsv4_unpack(qweight_packed, wbits, in_features)
+    out_f = q.shape[0]
+    s = np.asarray(scales, dtype=_F32)
+    z = np.asarray(qzeros, dtype=_F32)
+    if groupsize <= 0:
+        se, ze = s.reshape(out_f, 1), z.reshape(out_f, 1)
+    else:
+        G = (in_features + groupsize - 1) // groupsize
+        if s.shape == (out_f, G):
+            s, z = s.T, z.T
+        g = np.arange(in_features) // groupsize
+        se, ze = s[g, :].T, z[g, :].T
+    d = q.astype(_F32) - ze
+    return round_to((d * se).astype(_F32), dtype)
 
 
 # ---------------------------------------------------------------------------

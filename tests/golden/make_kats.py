@@ -13,7 +13,7 @@ import struct
 from fractions import Fraction
 from pathlib import Path
 
-FORMATS = {"bf16": (8, -126, 127), "f16": (11, -14, 15)}  # precision p, emin, emax
+FORMATS = {"bf16": (8, -126, 127), "f16": (11, -14, 15), "f32": (24, -126, 127)}  # precision p, emin, emax
 
 
 def rne(v: Fraction, fmt: str) -> Fraction:
@@ -111,6 +111,37 @@ def main() -> None:
 
     # 5. RTN nibble order: byte j -> (col 2j = low nibble, col 2j+1 = high nibble)
     kats["rtn_bytes"] = [{"byte": b, "cols": [b & 0xF, b >> 4]} for b in (0x00, 0x21, 0xF0, 0x0F, 0xA5, 0xFF)]
+
+    # 6. DSV4 uint8 packing along the in-dim: byte -> 8 // wbits codes, low bits first
+    kats["dsv4_bytes"] = [{"byte": b, "codes2": [(b >> (2 * i)) & 3 for i in range(4)],
+                           "codes4": [b & 0xF, b >> 4]} for b in (0x00, 0x1B, 0xE4, 0xFF, 0x80, 0x36)]
+
+    # 7. DSV4 dequant (layers/dsv4_packed_linear.py:22-56): in fp32,
+    #    d = RNE_f32(q - z), v = RNE_f32(d * s), then RNE to the output type;
+    #    z and s fp16 values (z not necessarily an integer; tiny ones make the
+    #    fp32 subtraction round).
+    dsv4 = []
+    special = [(2, 3, 2 ** -14 * (1 + 2 ** -10), 1.0), (4, 15, 2 ** -14 * (1 + 2 ** -10), 3.0 + 2 ** -9),
+               (4, 0, 0.5, 1.0), (2, 1, 1.5, 2 ** -24), (4, 7, 7.0, 65504.0)]
+    for wb, q, z, s_ in special:
+        dsv4.append((wb, q, f16_exact(z), f16_exact(s_)))
+    for _ in range(240):
+        wb = rnd.choice((2, 4))
+        q = rnd.randrange(1 << wb)
+        z = f16_exact(rnd.uniform(-1.0, (1 << wb) + 1.0)) if rnd.random() < 0.8 else f16_exact(
+            rnd.choice((1, -1)) * 2.0 ** rnd.randrange(-24, -10) * rnd.uniform(1, 2))
+        s_ = f16_exact(abs(rnd.gauss(0, 1)) * 0.02 + 1e-4)
+        dsv4.append((wb, q, z, s_))
+    recs = []
+    for wb, q, z, s_ in dsv4:
+        v = rne(rne(q - z, "f32") * s_, "f32")
+        def signed_bits(fmt):  # a negative value that rounds to zero is -0
+            r = out_bits(rne(v, fmt), fmt)
+            return r | 0x8000 if v < 0 else r
+
+        recs.append({"wbits": wb, "q": q, "zero_f16_bits": f16_bits(z), "scale_f16_bits": f16_bits(s_),
+                     "bf16_bits": signed_bits("bf16"), "f16_bits": signed_bits("f16")})
+    kats["dsv4_dequant"] = recs
 
     out = Path(__file__).with_name("kats.json")
     out.write_text(json.dumps(kats, indent=1))

@@ -24,6 +24,8 @@ DEV = "cuda:0"
     (1040, 3072, 26, True, False, torch.bfloat16, torch.float16),   # odd groups
     (1000, 64, 32, True, False, torch.bfloat16, torch.bfloat16),    # ragged K, bf16 scales
     (256, 64, 128, False, False, torch.float32, torch.float16),
+    (1024, 256, 32, True, True, torch.float16, torch.float32),     # fp32 scales: product rounded to fp32 first
+    (1024, 256, 32, True, False, torch.bfloat16, torch.float32),
 ])
 def test_gptq_dequant_bit_exact(K, N, gs, v1, act, out_dtype, scale_dtype):
     from onecomp_runtime import quant_utils, synthetic

@@ -358,3 +358,46 @@ def test_cpu_paths_gptq_linear_matches_oracle():
     ok, rel, cos = O.gemm_close(lin(x).float().numpy(), ref)
     assert ok, (rel, cos)
     assert torch.equal(lin.eager()(x), lin(x))
+
+
+# -- DSV4 uint8 packing (layers/dsv4_packed_linear.py:22-56) ---------------------
+def test_dsv4_byte_order_known_answers(kats):
+    for rec in kats["dsv4_bytes"]:
+        b = np.array([[rec["byte"]]], np.uint8)
+        assert O.dsv4_unpack(b, 2, 4)[0].tolist() == rec["codes2"]
+        assert O.dsv4_unpack(b, 4, 2)[0].tolist() == rec["codes4"]
+
+
+@pytest.mark.parametrize("fmt", ["bf16", "f16"])
+def test_dsv4_dequant_known_answers(kats, fmt):
+    for rec in kats["dsv4_dequant"]:
+        wb = rec["wbits"]
+        per = 8 // wb
+        codes = np.zeros((1, per), np.int64)
+        codes[0, 0] = rec["q"]
+        z = np.array([[rec["zero_f16_bits"]]], np.uint16).view(np.float16).astype(np.float32)
+        s = np.array([[rec["scale_f16_bits"]]], np.uint16).view(np.float16).astype(np.float32)
+        got = O.dequant_dsv4(O.dsv4_pack(codes, wb), s, z, wb, per, per, fmt)[0, 0]
+        want = rec[f"{fmt}_bits"]
+        assert (int(O.f32_to_bf16_bits(np.float32(got).reshape(1))[0]) if fmt == "bf16" else
+                int(np.float32(got).astype(np.float16).view(np.uint16))) == want, rec
+
+
+@pytest.mark.parametrize("wbits", [2, 4])
+def test_dsv4_pack_round_trip_and_orientation(wbits):
+    rng = np.random.default_rng(wbits)
+    out_f, k, gs = 24, 100, 32
+    codes = rng.integers(0, 1 << wbits, (out_f, k))
+    packed = O.dsv4_pack(codes, wbits)
+    assert packed.shape == (out_f, (k + 8 // wbits - 1) // (8 // wbits))
+    assert np.array_equal(O.dsv4_unpack(packed, wbits, k), codes)
+    G = (k + gs - 1) // gs
+    s = (np.abs(rng.standard_normal((G, out_f))) * 0.02 + 1e-4).astype(np.float16).astype(np.float32)
+    z = rng.uniform(0, 1 << wbits, (G, out_f)).astype(np.float16).astype(np.float32)
+    a = O.dequant_dsv4(packed, s, z, wbits, gs, k, "bf16")
+    b = O.dequant_dsv4(packed, s.T.copy(), z.T.copy(), wbits, gs, k, "bf16")
+    assert np.array_equal(a, b)
+    # brute force per element
+    n, kk = 5, 77
+    want = O.round_to(np.float32(np.float32(codes[n, kk] - z[kk // gs, n]) * s[kk // gs, n]), "bf16")
+    assert a[n, kk] == want
