@@ -390,6 +390,67 @@ int oc_dsv4_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t M,
 size_t oc_dsv4_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K);
 
 /*
+ * Packed int4 convolutions (layers/packed_conv.py:123-222), groups = 1, RTN
+ * weights as the reference's quantize_conv_weight writes them (:63-90):
+ * qweight uint8 [rows, row_bytes] nibbles (RTN order), scales / zeros
+ * [rows, G], dequant per op in x_dtype as dequant_extra_u8_to_weight.
+ *
+ * Conv1d: weight rows = C_out, columns ci * kernel_size + kk;
+ *   y[b, o, t] = bias[o] + sum_{ci, kk} Wd[o, ci * k + kk] *
+ *                x[b, ci, t * stride + kk * dilation - pad_left] (0 outside [0, L))
+ * x [B, C_in, L], y [B, C_out, T_out], fp32 accumulation, one rounding. The
+ * caller folds the reference's pad (_conv1d_pad, :93-105) and the conv's own
+ * padding into pad_left and T_out. Needs C_in * kernel_size % 32 == 0 and
+ * (C_in * kernel_size / G) % 8 == 0. Workspace >= oc_rtn_conv1d_workspace_bytes
+ * (a bounded chunk of im2col rows and fp32 partials).
+ */
+int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in,
+                  int32_t L, const uint8_t *qweight, int32_t row_bytes,
+                  const void *scales, int32_t scale_dtype, const void *zeros,
+                  int32_t zero_dtype, int32_t G, int32_t C_out,
+                  int32_t kernel_size, int32_t stride, int32_t dilation,
+                  int32_t pad_left, int32_t T_out, const void *bias,
+                  int32_t bias_dtype, void *y, void *workspace,
+                  size_t workspace_bytes, void *stream);
+size_t oc_rtn_conv1d_workspace_bytes(int32_t B, int32_t C_in, int32_t C_out,
+                                     int32_t kernel_size, int32_t T_out);
+
+/*
+ * Load time, ConvTranspose1d: the stored weight [rows = C_in, cols =
+ * C_out * kernel_size] (quant groups along cols) re-laid as
+ * qweight_t [cols, rows / 2] (RTN nibbles along C_in) and scales_t /
+ * zeros_t [G, rows] (16-bit); rows even.
+ */
+int oc_rtn_transpose_prepare(const uint8_t *qweight, int32_t rows,
+                             int32_t row_bytes, int32_t cols,
+                             const void *scales, const void *zeros, int32_t G,
+                             uint8_t *qweight_t, void *scales_t, void *zeros_t,
+                             void *stream);
+
+/*
+ * ConvTranspose1d over the re-laid weight:
+ *   y[b, o, t] = bias[o] + sum_{ci, kk, j: j * stride + kk * dilation - padding = t}
+ *                x[b, ci, j] * Wd[ci, o * k + kk]
+ * x [B, C_in, L_in], y [B, C_out, L_out] (L_out as torch's conv_transpose1d,
+ * output_padding included; the reference's unpad is a slice of y). Needs
+ * C_in % 32 == 0; scales_t / zeros_t of one 16-bit scale_dtype. Workspace >=
+ * oc_rtn_conv_transpose1d_workspace_bytes.
+ */
+int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B,
+                            int32_t C_in, int32_t L_in,
+                            const uint8_t *qweight_t, const void *scales_t,
+                            const void *zeros_t, int32_t scale_dtype, int32_t G,
+                            int32_t C_out, int32_t kernel_size, int32_t stride,
+                            int32_t dilation, int32_t padding, int32_t L_out,
+                            const void *bias, int32_t bias_dtype, void *y,
+                            void *workspace, size_t workspace_bytes,
+                            void *stream);
+size_t oc_rtn_conv_transpose1d_workspace_bytes(int32_t B, int32_t C_in,
+                                               int32_t L_in, int32_t C_out,
+                                               int32_t kernel_size,
+                                               int32_t L_out);
+
+/*
  * Device: MoE routing prologue (no reference counterpart: the reference has
  * no grouped GEMM; its MoE path loops over experts, layers/dsv4_packed_linear.py:95-98).
  * Stable counting sort of the T*topk (token, slot) pairs by expert id:

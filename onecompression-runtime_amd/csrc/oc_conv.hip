@@ -1,0 +1,350 @@
+// Packed int4 Conv1d / ConvTranspose1d (reference layers/packed_conv.py:123-222)
+// as GEMMs over the RTN nibble rows, for gfx950.
+//
+// Conv1d (groups = 1): out[b, o, t] = sum_{ci, kk} W[o, ci * k + kk] *
+// x[b, ci, t * stride + kk * dilation - pad_left]. Output positions are taken
+// in chunks of rows (b, t); each chunk's activation rows are written to the
+// workspace in the weight's column order (im2col, zeros outside [0, L)), the
+// LDS-tiled RTN kernel multiplies them into fp32 partials, and the epilogue
+// adds the K splits in order and the bias and rounds once into [B, O, T].
+//
+// ConvTranspose1d (groups = 1): out[b, o, t] = sum_{ci, kk, j : j * stride +
+// kk * dilation - padding = t} x[b, ci, j] W[ci, o * k + kk]. The stored rows
+// are input channels with quant groups along the output columns, so at load
+// time the codes are re-laid transposed (rows = output columns (o, kk), K =
+// ci) with the scales and zeros as [groups][C_in] (FMT_RTN_T reads the 8 K
+// rows' parameters of its lane). Per chunk of input positions j of one batch
+// row the GEMM gives Z[j, (o, kk)] in fp32; the scatter adds each output's
+// taps (kk ascending) into an fp32 accumulator, which the last pass rounds
+// with the bias. Chunks are added in order, so results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "oc_gemm_common.h"
+
+namespace oc {
+namespace {
+
+inline unsigned grid_1d(int64_t n, int block = 256) { return static_cast<unsigned>((n + block - 1) / block); }
+
+// A[r, c] (r < rows, c < K) for output rows r0 + r = b * T + t.
+__global__ __launch_bounds__(256) void im2col_kernel(const uint16_t *__restrict__ x, int C, int L, int k,
+                                                     int stride, int dilation, int pad_left, int T, int64_t r0,
+                                                     int rows, int K, uint16_t *__restrict__ a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(rows) * K) return;
+  const int c = static_cast<int>(idx % K);
+  const int64_t r = r0 + idx / K;
+  const int b = static_cast<int>(r / T), t = static_cast<int>(r % T);
+  const int ci = c / k, kk = c % k;
+  const int pos = t * stride + kk * dilation - pad_left;
+  a[idx] = (pos >= 0 && pos < L) ? x[(static_cast<int64_t>(b) * C + ci) * L + pos] : static_cast<uint16_t>(0);
+}
+
+// out[b, o, t] for the chunk's rows: the K splits of the fp32 partials in
+// order, plus bias, rounded once. t fastest (coalesced stores).
+template <int DT>
+__global__ __launch_bounds__(256) void conv1d_epilogue_kernel(const float *__restrict__ part, int ksplit, int rows,
+                                                              int N, int T, int64_t r0, const void *bias,
+                                                              int bias_dtype, void *__restrict__ y) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(rows) * N) return;
+  const int r = static_cast<int>(idx % rows);
+  const int n = static_cast<int>(idx / rows);
+  const int64_t mn = static_cast<int64_t>(rows) * N;
+  float v = 0.f;
+  for (int s = 0; s < ksplit; ++s) v += part[s * mn + static_cast<int64_t>(r) * N + n];
+  if (bias) v += load_any_f32(bias, n, bias_dtype);
+  const int64_t rr = r0 + r;
+  const int64_t b = rr / T, t = rr % T;
+  store_c<DT>(y, (b * N + n) * T + t, v);
+}
+
+// Transposed-weight re-layout: codes [C_in rows, cols] (RTN nibbles) ->
+// [cols rows, C_in / 2 bytes]; one thread per output byte (n, ci pair).
+__global__ __launch_bounds__(256) void rtn_transpose_kernel(const uint8_t *__restrict__ q, int rows, int row_bytes,
+                                                            int cols, uint8_t *__restrict__ qt) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int half = rows / 2;
+  if (idx >= static_cast<int64_t>(cols) * half) return;
+  const int n = static_cast<int>(idx / half), i = static_cast<int>(idx % half);
+  uint32_t v = 0;
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const int ci = 2 * i + e;
+    const uint8_t byte = q[static_cast<int64_t>(ci) * row_bytes + n / 2];
+    v |= ((n & 1) ? (byte >> 4) : (byte & 0xF)) << (4 * e);
+  }
+  qt[idx] = static_cast<uint8_t>(v);
+}
+
+// [rows, G] 16-bit -> [G, rows].
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t *__restrict__ in, int rows, int G,
+                                                          uint16_t *__restrict__ out) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(rows) * G) return;
+  const int g = static_cast<int>(idx / rows), r = static_cast<int>(idx % rows);
+  out[idx] = in[static_cast<int64_t>(r) * G + g];
+}
+
+// A[j, ci] = x[b, ci, j0 + j] for the chunk's input positions.
+__global__ __launch_bounds__(256) void positions_to_rows_kernel(const uint16_t *__restrict__ x, int C, int L, int b,
+                                                                int j0, int rows, uint16_t *__restrict__ a) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(rows) * C) return;
+  const int ci = static_cast<int>(idx % C);
+  const int j = static_cast<int>(idx / C);
+  a[idx] = x[(static_cast<int64_t>(b) * C + ci) * L + j0 + j];
+}
+
+// acc[o, t] += taps of input positions j0 .. j0 + rows - 1, kk ascending, for
+// t in [t_lo, t_hi). Z = the chunk's partials [ksplit][rows][O * k].
+__global__ __launch_bounds__(256) void col2im_add_kernel(const float *__restrict__ part, int ksplit, int rows, int O,
+                                                         int k, int stride, int dilation, int padding, int j0,
+                                                         int t_lo, int t_hi, int Lout, float *__restrict__ acc) {
+  const int span = t_hi - t_lo;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(span) * O) return;
+  const int t = t_lo + static_cast<int>(idx % span);
+  const int o = static_cast<int>(idx / span);
+  const int N = O * k;
+  const int64_t mn = static_cast<int64_t>(rows) * N;
+  float v = 0.f;
+  for (int kk = 0; kk < k; ++kk) {
+    const int num = t + padding - kk * dilation;
+    if (num < 0 || num % stride != 0) continue;
+    const int j = num / stride - j0;
+    if (j < 0 || j >= rows) continue;
+    for (int s = 0; s < ksplit; ++s) v += part[s * mn + static_cast<int64_t>(j) * N + o * k + kk];
+  }
+  acc[static_cast<int64_t>(o) * Lout + t] += v;
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void finish_kernel(const float *__restrict__ acc, int O, int Lout, const void *bias,
+                                                     int bias_dtype, void *__restrict__ y) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(O) * Lout) return;
+  const int o = static_cast<int>(idx / Lout);
+  float v = acc[idx];
+  if (bias) v += load_any_f32(bias, o, bias_dtype);
+  store_c<DT>(y, idx, v);
+}
+
+__global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, int64_t n) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx < n) p[idx] = 0.f;
+}
+
+// Rows per chunk: a bounded workspace (activation rows plus fp32 partials).
+constexpr size_t CONV_CHUNK_BYTES = size_t{64} << 20;
+
+int chunk_rows(int64_t total, int K, int N) {
+  const int64_t per_row = 2 * static_cast<int64_t>(K) + 4 * static_cast<int64_t>(N);
+  int64_t r = std::max<int64_t>(256, static_cast<int64_t>(CONV_CHUNK_BYTES) / per_row) / 256 * 256;
+  return static_cast<int>(std::min<int64_t>(total, r));
+}
+
+// Workspace of one chunk of `rows` rows: activations, then fp32 partials.
+size_t chunk_bytes(int rows, int K, int N) {
+  int wm, wn, ksplit, kps;
+  plan_tiled(rows, N, K, &wm, &wn, &ksplit, &kps);
+  const size_t a = (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256;
+  return a + static_cast<size_t>(ksplit) * rows * N * sizeof(float);
+}
+
+size_t conv_chunks_bytes(int64_t total, int K, int N) {
+  if (total <= 0) return 0;
+  const int r = chunk_rows(total, K, N);
+  const int rem = static_cast<int>(total % r);
+  return std::max(chunk_bytes(r, K, N), rem ? chunk_bytes(rem, K, N) : size_t{0});
+}
+
+// One chunk's GEMM: A [rows, K] (in the workspace) times the packed rows into
+// fp32 partials right after A. Returns the K splits.
+int chunk_gemm(const void *a, int x_dtype, int rows, int K, const uint8_t *q, int row_bytes, const void *scales,
+               int scale_dtype, const void *zeros, int zero_dtype, int gs, int64_t stride_n, int64_t stride_g,
+               int N, bool transposed, float *part, hipStream_t s) {
+  int wm, wn, ksplit, kps;
+  plan_tiled(rows, N, K, &wm, &wn, &ksplit, &kps);
+  GemmParams p{};
+  p.a = a;
+  p.lda = K;
+  p.M = rows;
+  p.K_logical = K;
+  p.qw = q;
+  p.scales = scales;
+  p.zeros = zeros;
+  p.scale_dtype = scale_dtype;
+  p.zero_dtype = zero_dtype;
+  p.rtn_gs = gs;
+  p.rtn_G = K / gs;
+  p.row_bytes = row_bytes;
+  p.sz_stride_n = stride_n;
+  p.sz_stride_g = stride_g;
+  p.N = N;
+  p.K_phys = K;
+  p.KS = K / 32;
+  p.group_rows = 32;
+  p.gshift = 0;
+  p.partials = part;
+  p.out_f32 = 1;
+  p.ksplit = ksplit;
+  p.ksteps_per_split = kps;
+  launch_rtn_tiled(p, x_dtype, transposed, wm, wn, s);
+  return ksplit;
+}
+
+}  // namespace
+}  // namespace oc
+
+using namespace oc;
+
+extern "C" {
+
+size_t oc_rtn_conv1d_workspace_bytes(int32_t B, int32_t C_in, int32_t C_out, int32_t kernel_size, int32_t T_out) {
+  const int64_t K = static_cast<int64_t>(C_in) * kernel_size;
+  if (B <= 0 || T_out <= 0 || K <= 0 || K > (1 << 30)) return 0;
+  return conv_chunks_bytes(static_cast<int64_t>(B) * T_out, static_cast<int>(K), C_out);
+}
+
+int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32_t L, const uint8_t *qweight,
+                  int32_t row_bytes, const void *scales, int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
+                  int32_t G, int32_t C_out, int32_t kernel_size, int32_t stride, int32_t dilation, int32_t pad_left,
+                  int32_t T_out, const void *bias, int32_t bias_dtype, void *y, void *workspace,
+                  size_t workspace_bytes, void *stream) {
+  clear_error();
+  if (B < 0 || C_in <= 0 || L < 0 || C_out <= 0 || kernel_size <= 0 || stride <= 0 || dilation <= 0 || T_out < 0 ||
+      G <= 0)
+    return fail(OC_ERR_SHAPE, "bad conv shape");
+  if (B == 0 || T_out == 0) return OC_OK;
+  if (!x || !qweight || !scales || !zeros || !y) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!is_half_dtype(x_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "x_dtype must be F16 or BF16");
+  if (!is_float_dtype(scale_dtype) || dtype_bytes(zero_dtype) == 0)
+    return fail(OC_ERR_INVALID_ARGUMENT, "unsupported scale/zero dtype");
+  if (bias && !is_float_dtype(bias_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "bad bias dtype");
+  const int64_t K64 = static_cast<int64_t>(C_in) * kernel_size;
+  if (K64 % 32 != 0 || K64 % G != 0 || (K64 / G) % 8 != 0 || row_bytes < K64 / 2 || row_bytes % 4 != 0)
+    return fail(OC_ERR_UNSUPPORTED,
+                "fused conv1d needs C_in * kernel_size %% 32 == 0, groups of a multiple of 8 columns and "
+                "4-byte weight rows (K=%lld G=%d row_bytes=%d)", static_cast<long long>(K64), G, row_bytes);
+  const int K = static_cast<int>(K64);
+  const int64_t total = static_cast<int64_t>(B) * T_out;
+  const size_t need = conv_chunks_bytes(total, K, C_out);
+  if (!workspace || workspace_bytes < need)
+    return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!aligned(workspace, 256) || !aligned(qweight, 4)) return fail(OC_ERR_SHAPE, "misaligned workspace or weight");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int R = chunk_rows(total, K, C_out);
+  for (int64_t r0 = 0; r0 < total; r0 += R) {
+    const int rows = static_cast<int>(std::min<int64_t>(R, total - r0));
+    uint16_t *a = static_cast<uint16_t *>(workspace);
+    float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) +
+                                            (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256);
+    hipLaunchKernelGGL(im2col_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * K)), dim3(256), 0, s,
+                       static_cast<const uint16_t *>(x), C_in, L, kernel_size, stride, dilation, pad_left, T_out, r0,
+                       rows, K, a);
+    const int ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype,
+                                  K / G, G, 1, C_out, false, part, s);
+    const dim3 grid(grid_1d(static_cast<int64_t>(rows) * C_out));
+    if (x_dtype == OC_DTYPE_BF16)
+      hipLaunchKernelGGL(conv1d_epilogue_kernel<OC_DTYPE_BF16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
+                         T_out, r0, bias, bias_dtype, y);
+    else
+      hipLaunchKernelGGL(conv1d_epilogue_kernel<OC_DTYPE_F16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
+                         T_out, r0, bias, bias_dtype, y);
+  }
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_rtn_transpose_prepare(const uint8_t *qweight, int32_t rows, int32_t row_bytes, int32_t cols,
+                             const void *scales, const void *zeros, int32_t G, uint8_t *qweight_t, void *scales_t,
+                             void *zeros_t, void *stream) {
+  clear_error();
+  if (!qweight || !scales || !zeros || !qweight_t || !scales_t || !zeros_t)
+    return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (rows <= 0 || rows % 2 != 0 || cols <= 0 || row_bytes < (cols + 1) / 2 || G <= 0)
+    return fail(OC_ERR_SHAPE, "bad shape rows=%d cols=%d row_bytes=%d G=%d", rows, cols, row_bytes, G);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(rtn_transpose_kernel, dim3(grid_1d(static_cast<int64_t>(cols) * (rows / 2))), dim3(256), 0, s,
+                     qweight, rows, row_bytes, cols, qweight_t);
+  const dim3 g(grid_1d(static_cast<int64_t>(rows) * G));
+  hipLaunchKernelGGL(transpose16_kernel, g, dim3(256), 0, s, static_cast<const uint16_t *>(scales), rows, G,
+                     static_cast<uint16_t *>(scales_t));
+  hipLaunchKernelGGL(transpose16_kernel, g, dim3(256), 0, s, static_cast<const uint16_t *>(zeros), rows, G,
+                     static_cast<uint16_t *>(zeros_t));
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+size_t oc_rtn_conv_transpose1d_workspace_bytes(int32_t B, int32_t C_in, int32_t L_in, int32_t C_out,
+                                               int32_t kernel_size, int32_t L_out) {
+  if (B <= 0 || L_in <= 0 || C_in <= 0 || C_out <= 0 || kernel_size <= 0 || L_out <= 0) return 0;
+  const int N = C_out * kernel_size;
+  const size_t acc = (static_cast<size_t>(C_out) * L_out * sizeof(float) + 255) / 256 * 256;
+  return acc + conv_chunks_bytes(L_in, C_in, N);
+}
+
+int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32_t L_in,
+                            const uint8_t *qweight_t, const void *scales_t, const void *zeros_t, int32_t scale_dtype,
+                            int32_t G, int32_t C_out, int32_t kernel_size, int32_t stride, int32_t dilation,
+                            int32_t padding, int32_t L_out, const void *bias, int32_t bias_dtype, void *y,
+                            void *workspace, size_t workspace_bytes, void *stream) {
+  clear_error();
+  if (B < 0 || C_in <= 0 || L_in < 0 || C_out <= 0 || kernel_size <= 0 || stride <= 0 || dilation <= 0 ||
+      L_out < 0 || G <= 0 || padding < 0)
+    return fail(OC_ERR_SHAPE, "bad conv-transpose shape");
+  if (B == 0 || L_in == 0 || L_out == 0) return OC_OK;
+  if (!x || !qweight_t || !scales_t || !zeros_t || !y) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (!is_half_dtype(x_dtype) || !is_half_dtype(scale_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "x and scales/zeros must be F16 or BF16");
+  if (bias && !is_float_dtype(bias_dtype)) return fail(OC_ERR_INVALID_ARGUMENT, "bad bias dtype");
+  const int N = C_out * kernel_size;
+  if (C_in % 32 != 0 || N % G != 0)
+    return fail(OC_ERR_UNSUPPORTED, "fused conv-transpose needs C_in %% 32 == 0 and groups dividing the columns");
+  const size_t need = oc_rtn_conv_transpose1d_workspace_bytes(B, C_in, L_in, C_out, kernel_size, L_out);
+  if (!workspace || workspace_bytes < need)
+    return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
+                workspace ? workspace_bytes : static_cast<size_t>(0));
+  if (!aligned(workspace, 256) || !aligned(qweight_t, 4) || !aligned(scales_t, 16) || !aligned(zeros_t, 16))
+    return fail(OC_ERR_SHAPE, "misaligned workspace or weights");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float *acc = static_cast<float *>(workspace);
+  char *chunk_ws = static_cast<char *>(workspace) + (static_cast<size_t>(C_out) * L_out * 4 + 255) / 256 * 256;
+  const int R = chunk_rows(L_in, C_in, N);
+  const int64_t outs = static_cast<int64_t>(C_out) * L_out;
+  const int span_max = (R - 1) * stride + (kernel_size - 1) * dilation + 1;
+  for (int b = 0; b < B; ++b) {
+    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_1d(outs)), dim3(256), 0, s, acc, outs);
+    for (int j0 = 0; j0 < L_in; j0 += R) {
+      const int rows = std::min(R, L_in - j0);
+      uint16_t *a = reinterpret_cast<uint16_t *>(chunk_ws);
+      float *part = reinterpret_cast<float *>(chunk_ws + (static_cast<size_t>(rows) * C_in * 2 + 255) / 256 * 256);
+      hipLaunchKernelGGL(positions_to_rows_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * C_in)), dim3(256), 0, s,
+                         static_cast<const uint16_t *>(x), C_in, L_in, b, j0, rows, a);
+      const int ksplit = chunk_gemm(a, x_dtype, rows, C_in, qweight_t, C_in / 2, scales_t, scale_dtype, zeros_t,
+                                    scale_dtype, N / G, 0, 0, N, true, part, s);
+      const int t_lo = std::max(0, j0 * stride - padding);
+      const int t_hi = std::min(L_out, (j0 + rows - 1) * stride + (kernel_size - 1) * dilation - padding + 1);
+      if (t_hi <= t_lo) continue;
+      (void)span_max;
+      hipLaunchKernelGGL(col2im_add_kernel, dim3(grid_1d(static_cast<int64_t>(t_hi - t_lo) * C_out)), dim3(256), 0,
+                         s, part, ksplit, rows, C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi, L_out,
+                         acc);
+    }
+    void *yb = static_cast<char *>(y) + static_cast<size_t>(b) * outs * 2;
+    if (x_dtype == OC_DTYPE_BF16)
+      hipLaunchKernelGGL(finish_kernel<OC_DTYPE_BF16>, dim3(grid_1d(outs)), dim3(256), 0, s, acc, C_out, L_out, bias,
+                         bias_dtype, yb);
+    else
+      hipLaunchKernelGGL(finish_kernel<OC_DTYPE_F16>, dim3(grid_1d(outs)), dim3(256), 0, s, acc, C_out, L_out, bias,
+                         bias_dtype, yb);
+  }
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+}  // extern "C"

@@ -507,6 +507,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   uint32_t sa[PF][A_PER_THREAD * 4];
   uint32_t sq[PF][WN], ss[PF][WN], sz[PF][WN];
   uint32_t sq8[PF][WN];  // 8-bit: the second word of the lane's 8 codes
+  uint32_t sst[PF][WN][4], szt[PF][WN][4];  // RTN_T: the 8 K rows' scales / zeros (16-bit pairs)
   auto load = [&](auto fc, int ks) __attribute__((always_inline)) {
     constexpr int f = decltype(fc)::value;
     ks = min(ks, max(ks_end - 1, 0));
@@ -534,6 +535,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
         continue;
       }
       sq[f][j] = load_word<FMT>(p, p.qw, tl, ks, quad, c16);
+      if constexpr (FMT == FMT_RTN_T) {
+        // Scales / zeros of K rows 32 ks + 8 quad .. +7 in the group of column n.
+        const int n = min(TILE_N * tl + c16, p.N - 1);
+        const int64_t i = static_cast<int64_t>(n / p.rtn_gs) * p.K_logical + 32 * ks + 8 * quad;
+        const uint4 sv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.scales) + i);
+        const uint4 zv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.zeros) + i);
+        sst[f][j][0] = sv.x; sst[f][j][1] = sv.y; sst[f][j][2] = sv.z; sst[f][j][3] = sv.w;
+        szt[f][j][0] = zv.x; szt[f][j][1] = zv.y; szt[f][j][2] = zv.z; szt[f][j][3] = zv.w;
+        continue;
+      }
       if constexpr (FMT == FMT_GPTQ) {
         const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
         ss[f][j] = static_cast<const uint16_t *>(p.scales)[tgs * TILE_N + c16];
@@ -589,6 +600,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
             const float sv = scale_f32<SDT>(ss[f][j]);
             const float zv = static_cast<float>((sz[f][j] >> (8 * (c16 & 3))) & 0xFFu);
             b[j] = dequant8_u8<DT>(sq[f][j], sq8[f][j], sv, -sv * zv);
+          } else if constexpr (FMT == FMT_RTN_T) {
+            float v[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              RtnParam rp;
+              rp.sq = round_to<DT>(half_to_f32<RDT>((sst[f][j][e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+              rp.zq = round_to<DT>(half_to_f32<RDT>((szt[f][j][e >> 1] >> (16 * (e & 1))) & 0xFFFFu));
+              v[e] = rtn_value<DT>(static_cast<int>((sq[f][j] >> (4 * e)) & 0xFu), rp);
+            }
+            b[j] = uint4{pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]), pack2<DT>(v[6], v[7])};
           } else if constexpr (FMT == FMT_DSV4_4 || FMT == FMT_DSV4_2) {
             float sv, zv;
             if constexpr (RDT != 0) {
@@ -625,7 +646,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   }
 
   // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
-  if (p.ksplit == 1) {
+  if (p.ksplit == 1 && !p.out_f32) {
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = TILE_N * (tw + j) + c16;
@@ -640,7 +661,7 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
         }
     }
   } else {
-    // split-K: fp32 partials; splitk_reduce_kernel sums them in split order
+    // split-K (or fp32 output): fp32 partials; the caller's reduce sums them in split order
     float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
@@ -1356,7 +1377,7 @@ void launch_tiled_t(const GemmParams &p, hipStream_t s) {
                        0, s, p);
   else
     hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0>), grid, dim3(256), 0, s, p);
-  if (p.ksplit > 1) {
+  if (p.ksplit > 1 && !p.out_f32) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
     hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0,
                        s, p);
@@ -1432,6 +1453,26 @@ Plan plan_tiled_only(int M, int N, int K_phys, bool has_kmap) {
   sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
   sp.gather = has_kmap;
   return sp;
+}
+
+void plan_tiled(int M, int N, int K, int *wm, int *wn, int *ksplit, int *ksteps_per_split) {
+  const Plan sp = plan_tiled_only(M, N, K, false);
+  *wm = sp.tile.wm;
+  *wn = sp.tile.wn;
+  *ksplit = sp.ksplit;
+  *ksteps_per_split = sp.ksteps_per_split;
+}
+
+void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, hipStream_t s) {
+  const TileCfg c{wm, wn};
+  const bool bf = x_dtype == OC_DTYPE_BF16;
+  if (transposed) {
+    if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN_T>(p, c, s);
+    else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_RTN_T>(p, c, s);
+  } else {
+    if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN>(p, c, s);
+    else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_RTN>(p, c, s);
+  }
 }
 
 }  // namespace oc

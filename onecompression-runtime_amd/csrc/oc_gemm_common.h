@@ -17,8 +17,11 @@ namespace oc {
 // [N, K/2], 8-bit GPTQ tile16 (32 code bytes per column and K step).
 // DSV4: uint8 [N, K / per] codes along the in-dim (int4: the RTN nibble
 // order; int2: 4 codes per byte, low bits first), fp32 dequant (q - z) * s.
-enum { FMT_GPTQ = 0, FMT_RTN = 1, FMT_GPTQ8 = 2, FMT_DSV4_4 = 3, FMT_DSV4_2 = 4 };
-constexpr bool fmt_rows(int f) { return f == FMT_RTN || f == FMT_DSV4_4 || f == FMT_DSV4_2; }
+// RTN_T: RTN nibbles of a transposed weight (rows = output columns n, K
+// along each row) whose scales and zeros vary along K: one per (K row, group
+// of n), stored [groups][K] (the packed ConvTranspose1d weight).
+enum { FMT_GPTQ = 0, FMT_RTN = 1, FMT_GPTQ8 = 2, FMT_DSV4_4 = 3, FMT_DSV4_2 = 4, FMT_RTN_T = 5 };
+constexpr bool fmt_rows(int f) { return f == FMT_RTN || f == FMT_DSV4_4 || f == FMT_DSV4_2 || f == FMT_RTN_T; }
 
 struct GemmParams {
   const void *a;
@@ -48,6 +51,7 @@ struct GemmParams {
   void *c;
   int64_t ldc;
   float *partials;  // fp32 partial sums [ksplit, M, N] (split-K)
+  int out_f32;      // 1: the tiled kernel writes fp32 partials even without a K split
   int ksplit;
   int ksteps_per_split;
   // grouped (MoE) launch
@@ -194,6 +198,13 @@ __device__ __forceinline__ uint4 octet_pairs(uint4 raw, float &sum) {
 
 // Host helpers.
 int env_int(const char *name, int dflt);
+
+// LDS-tiled kernel over RTN nibble rows (oc_gemm.hip): tile shape and K split
+// for an M x N x K problem, and a launch of FMT_RTN (transposed = false) or
+// FMT_RTN_T. With p.out_f32 (or a K split) the kernel writes fp32 partials
+// [ksplit][M][N] to p.partials and nothing else.
+void plan_tiled(int M, int N, int K, int *wm, int *wn, int *ksplit, int *ksteps_per_split);
+void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, hipStream_t s);
 
 // Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
 // ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.

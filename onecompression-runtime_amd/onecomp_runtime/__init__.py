@@ -18,9 +18,12 @@ from .layers import (
     GemLiteInt4Linear,
     PackedEmbedding,
     PackedGPTQLinear,
+    PackedInt4Conv1d,
+    PackedInt4ConvTranspose1d,
     PackedRTNLinear,
     fused_int4_gemm,
     gemlite_available,
+    replace_conv_with_packed,
 )
 
 __version__ = "0.1.0"
@@ -36,6 +39,9 @@ __all__ = [
     "PackedGPTQLinear",
     "PackedRTNLinear",
     "PackedEmbedding",
+    "PackedInt4Conv1d",
+    "PackedInt4ConvTranspose1d",
+    "replace_conv_with_packed",
     "backend",
     "kernels",
     "quant_utils",

@@ -137,6 +137,19 @@ SIGNATURES = {
          _P, _I32, _P, _I64, _P, _SZ, _P],
     ),
     "oc_dsv4_gemm_workspace_bytes": (_SZ, [_I32, _I32, _I32]),
+    "oc_rtn_conv1d": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, _I32, _P, _I32, _P, _I32, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+         _I32, _P, _I32, _P, _P, _SZ, _P],
+    ),
+    "oc_rtn_conv1d_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32]),
+    "oc_rtn_transpose_prepare": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P, _P]),
+    "oc_rtn_conv_transpose1d": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+         _P, _I32, _P, _P, _SZ, _P],
+    ),
+    "oc_rtn_conv_transpose1d_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "oc_moe_route": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _P]),
     "oc_int4_moe_gemm": (
         ctypes.c_int,

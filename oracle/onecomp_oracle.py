@@ -24,6 +24,7 @@ How each function is pinned (tests/test_oracle.py):
                                order, fp32 sub and mul rounding, output rounding),
                                pack/unpack round trip, orientation identity
     embedding               -> row gather identity + output-dtype rule
+    conv1d / conv_transpose -> torch's float64 F.conv1d / F.conv_transpose1d
     linear / gptq_linear    -> float64 brute force on tiny shapes; act-order and
                                padded-groups invariances
     moe                     -> per-pair brute force
@@ -260,6 +261,49 @@ def dequant_dsv4(qweight_packed, scales, qzeros, wbits: int, groupsize: int, in_
         se, ze = s[g, :].T, z[g, :].T
     d = q.astype(_F32) - ze
     return round_to((d * se).astype(_F32), dtype)
+
+
+# ---------------------------------------------------------------------------
+# Convolutions (F.conv1d / F.conv_transpose1d with groups = 1, as the packed
+# conv layers call them after dequant, layers/packed_conv.py:162-170, :211-222)
+def conv1d(x, weight, bias, stride: int, dilation: int, pad_left: int, T: int, out_dtype: str) -> np.ndarray:
+    """y[b, o, t] = bias[o] + sum_{ci, kk} w[o, ci, kk] x[b, ci, t s + kk d - pad_left]
+    (zeros outside the input), fp32 accumulation, one rounding."""
+    x = np.asarray(x, dtype=_F32)
+    w = np.asarray(weight, dtype=_F32)
+    B, C, L = x.shape
+    O, _, k = w.shape
+    y = np.zeros((B, O, T), dtype=_F32)
+    t = np.arange(T)
+    for kk in range(k):
+        pos = t * stride + kk * dilation - pad_left
+        ok = (pos >= 0) & (pos < L)
+        xs = np.zeros((B, C, T), dtype=_F32)
+        xs[:, :, ok] = x[:, :, pos[ok]]
+        y += np.matmul(w[:, :, kk], xs)  # [O, C] @ [B, C, T]
+    if bias is not None:
+        y += np.asarray(bias, dtype=_F32)[None, :, None]
+    return round_to(y, out_dtype)
+
+
+def conv_transpose1d(x, weight, bias, stride: int, dilation: int, padding: int, L_out: int,
+                     out_dtype: str) -> np.ndarray:
+    """y[b, o, t] = bias[o] + sum_{ci, kk, j : j s + kk d - padding = t} w[ci, o, kk] x[b, ci, j],
+    fp32 accumulation, one rounding. weight [C_in, C_out, k]."""
+    x = np.asarray(x, dtype=_F32)
+    w = np.asarray(weight, dtype=_F32)
+    B, C, L = x.shape
+    _, O, k = w.shape
+    y = np.zeros((B, O, L_out), dtype=_F32)
+    j = np.arange(L)
+    for kk in range(k):
+        t = j * stride + kk * dilation - padding
+        ok = (t >= 0) & (t < L_out)
+        contrib = np.matmul(np.ascontiguousarray(w[:, :, kk].T), x)  # [O, C] @ [B, C, L]
+        np.add.at(y, (slice(None), slice(None), t[ok]), contrib[:, :, ok])
+    if bias is not None:
+        y += np.asarray(bias, dtype=_F32)[None, :, None]
+    return round_to(y, out_dtype)
 
 
 # ---------------------------------------------------------------------------

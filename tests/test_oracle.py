@@ -401,3 +401,50 @@ def test_dsv4_pack_round_trip_and_orientation(wbits):
     n, kk = 5, 77
     want = O.round_to(np.float32(np.float32(codes[n, kk] - z[kk // gs, n]) * s[kk // gs, n]), "bf16")
     assert a[n, kk] == want
+
+
+@pytest.mark.parametrize("stride,dilation,pad", [(1, 1, 0), (2, 1, 3), (3, 2, 4)])
+def test_conv_oracles_match_torch_float64(stride, dilation, pad):
+    import torch
+
+    rng = np.random.default_rng(stride * 10 + dilation)
+    B, C, Co, L, k = 2, 5, 6, 23, 4
+    x = rng.standard_normal((B, C, L)).astype(np.float32)
+    w = rng.standard_normal((Co, C, k)).astype(np.float32)
+    b = rng.standard_normal(Co).astype(np.float32)
+    T = (L + 2 * pad - dilation * (k - 1) - 1) // stride + 1
+    got = O.conv1d(x, w, b, stride, dilation, pad, T, "f32")
+    ref = torch.nn.functional.conv1d(torch.from_numpy(x).double(), torch.from_numpy(w).double(),
+                                     torch.from_numpy(b).double(), stride, pad, dilation).numpy()
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
+    wt = rng.standard_normal((C, Co, k)).astype(np.float32)
+    for op in (0, stride - 1):
+        L_out = (L - 1) * stride - 2 * pad + dilation * (k - 1) + op + 1
+        got = O.conv_transpose1d(x, wt, b, stride, dilation, pad, L_out, "f32")
+        ref = torch.nn.functional.conv_transpose1d(torch.from_numpy(x).double(), torch.from_numpy(wt).double(),
+                                                   torch.from_numpy(b).double(), stride, pad, op, 1,
+                                                   dilation).numpy()
+        assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_conv_quantizer_and_nibbles_host():
+    """Host helpers of the packed conv layers: nibble order (the RTN order),
+    and the RTN conv quantizer reconstructs within half a step."""
+    import torch
+
+    from onecomp_runtime.layers import pack_int4_nibbles, quantize_conv_weight, unpack_int4_nibbles
+
+    codes = torch.randint(0, 16, (7, 13), generator=torch.Generator().manual_seed(0))
+    packed = pack_int4_nibbles(codes)
+    assert np.array_equal(packed.numpy(), O.rtn_pack(codes.numpy()))
+    assert torch.equal(unpack_int4_nibbles(packed, 13).long(), codes)
+    w = torch.randn(6, 64, generator=torch.Generator().manual_seed(1))
+    w[2] = 0.0
+    for gs in (32, -1, 48):
+        q, s, z, cols = quantize_conv_weight(w, groupsize=gs)
+        G = 2 if gs == 32 else 1
+        assert cols == 64 and s.shape == (6, G) and s.dtype == torch.float16 and z.dtype == torch.float16
+        wd = O.rtn_dequant(q.numpy(), s.float().numpy(), z.float().numpy(), 64, 6, "f32")
+        step = np.repeat(s.float().numpy(), 64 // G, axis=1)
+        assert (np.abs(wd - w.numpy()) <= 0.5 * step + 2e-3 * np.abs(w.numpy()) + 1e-3).all()
+        assert (wd[2] == 0).all()
