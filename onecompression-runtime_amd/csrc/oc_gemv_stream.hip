@@ -131,7 +131,18 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   auto stage_load = [&](int base) {
 #pragma unroll
     for (int u = 0; u < SB; ++u) {
-      const int ic = min(base + SNT * u + tid, n_items - 1);  // clamped: every thread loads
+      // Waves wholly past the end load nothing (their registers are never
+      // stored); the lanes of a wave past the end read the last octet.
+      // (Every workgroup stages the same rows at once: whole waves of
+      // redundant loads of one line queue on one L2 channel. Measured on the
+      // K = 5120 decode layers, 640 octets in 3 x 1024 slots: -0.3 us.)
+      if (base + SNT * u + (tid & ~63) >= n_items) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) xr[m][u] = make_uint4(0, 0, 0, 0);
+        rr[u] = make_uint4(0, 0, 0, 0);
+        continue;
+      }
+      const int ic = min(base + SNT * u + tid, n_items - 1);
       if constexpr (SX == SX_GATHER) {
         const int4 k0 = *reinterpret_cast<const int4 *>(p.kmap + 8 * ic);
         const int4 k1 = *reinterpret_cast<const int4 *>(p.kmap + 8 * ic + 4);
