@@ -148,8 +148,8 @@ int chunk_rows(int64_t total, int K, int N) {
 
 // Workspace of one chunk of `rows` rows: activations, then fp32 partials.
 size_t chunk_bytes(int rows, int K, int N) {
-  int wm, wn, ksplit, kps;
-  plan_tiled(rows, N, K, &wm, &wn, &ksplit, &kps);
+  int wm, wn, kg, ksplit, kps;
+  plan_tiled(rows, N, K, &wm, &wn, &kg, &ksplit, &kps);
   const size_t a = (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256;
   return a + static_cast<size_t>(ksplit) * rows * N * sizeof(float);
 }
@@ -166,8 +166,8 @@ size_t conv_chunks_bytes(int64_t total, int K, int N) {
 int chunk_gemm(const void *a, int x_dtype, int rows, int K, const uint8_t *q, int row_bytes, const void *scales,
                int scale_dtype, const void *zeros, int zero_dtype, int gs, int64_t stride_n, int64_t stride_g,
                int N, bool transposed, float *part, hipStream_t s) {
-  int wm, wn, ksplit, kps;
-  plan_tiled(rows, N, K, &wm, &wn, &ksplit, &kps);
+  int wm, wn, kg, ksplit, kps;
+  plan_tiled(rows, N, K, &wm, &wn, &kg, &ksplit, &kps);
   GemmParams p{};
   p.a = a;
   p.lda = K;
@@ -192,7 +192,7 @@ int chunk_gemm(const void *a, int x_dtype, int rows, int K, const uint8_t *q, in
   p.out_f32 = 1;
   p.ksplit = ksplit;
   p.ksteps_per_split = kps;
-  launch_rtn_tiled(p, x_dtype, transposed, wm, wn, s);
+  launch_rtn_tiled(p, x_dtype, transposed, wm, wn, kg, s);
   return ksplit;
 }
 

@@ -233,6 +233,30 @@ __device__ __forceinline__ uint4 rtn_dequant8(uint32_t q, RtnParam p) {
   return r;
 }
 
+// Exact shortcut of rtn_dequant8 for 16-bit DT. With an integral zero
+// |zq| <= 240 and a scale 2^-100 < sq < 2^100: c - zq is an integer of at
+// most 8 bits (exact in bf16 and fp16, so the first rounding is the
+// identity), (c - zq) sq and zq sq have at most 19 significant bits (exact in
+// fp32), so fma(c, sq, -zq sq) is the exact product and the pack rounds it
+// once, as the reference's second rounding does. A positive scale also gives
+// the same signed zeros (c = zq: +0 either way).
+template <int DT>
+__device__ __forceinline__ bool rtn_fast_ok(RtnParam p) {
+  return p.zq == __builtin_rintf(p.zq) && __builtin_fabsf(p.zq) <= 240.f && p.sq > 0x1p-100f && p.sq < 0x1p100f;
+}
+template <int DT>
+__device__ __forceinline__ uint4 rtn_dequant8_fast(uint32_t q, RtnParam p) {
+  const float nzs = -p.zq * p.sq;
+  const uint32_t lo = q & 0x0F0F0F0Fu, hi = (q >> 4) & 0x0F0F0F0Fu;  // codes 0 2 4 6 | 1 3 5 7
+  float f[8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __builtin_fmaf(static_cast<float>((lo >> (8 * i)) & 0xFFu), p.sq, nzs);
+    f[2 * i + 1] = __builtin_fmaf(static_cast<float>((hi >> (8 * i)) & 0xFFu), p.sq, nzs);
+  }
+  return uint4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
+}
+
 // ---- MFMA -----------------------------------------------------------------------
 //
 // v_mfma_f32_16x16x32_{bf16,f16} operand layout (one wave, lane l):

@@ -462,14 +462,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
 }
 
 // ---------------------------------------------------------------------------
-// LDS-tiled kernel. BM = 16*WM rows, BN = 64*WN columns (4 waves x WN tiles).
-// grid = (ceil(N/BN), ceil(M/BM), ksplit).
+// LDS-tiled kernel. BM = 16*WM rows, BN = 64*WN columns (4 waves x WN tiles),
+// KG groups of 4 waves per workgroup splitting the workgroup's K steps into
+// contiguous parts (each group its own LDS tiles; the groups' sums are added
+// in group order at the end). One wave per SIMD leaves every latency of a
+// step exposed; KG = 4 puts four independent steps on each SIMD.
+// grid = (ceil(N/BN), ceil(M/BM), ksplit), 256 KG threads.
 constexpr int A_LDS_STRIDE = 40;  // halves per LDS row: 32 data + 8 pad (80 B)
 
 // RDT (RTN): the dtype of both scales and zeros when they share a 16-bit one
 // (raw loads, converted at use), else 0 (any dtypes, converted as loaded).
-template <int DT, int SDT, int WM, int WN, int FMT, int RDT>
-__global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
+template <int DT, int SDT, int WM, int WN, int FMT, int RDT, int KG>
+__global__ __launch_bounds__(256 * KG) void gemm_tiled_kernel(GemmParams p) {
   // PF K steps in flight in registers (activation chunks, weight words and
   // group parameters of each step); the activation tile of the next step is
   // written to the other LDS buffer once its loads are in, and the step ends
@@ -479,8 +483,9 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   constexpr int BM = 16 * WM;
   constexpr int BN = 64 * WN;
   constexpr int PF = 2;  // measured on RTN M=512: 2 beats 4 and 8
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][BM * A_LDS_STRIDE];
-  const int tid = threadIdx.x;
+  __shared__ __attribute__((aligned(16))) uint16_t As_all[KG][2][BM * A_LDS_STRIDE];
+  const int tid = threadIdx.x & 255, grp = threadIdx.x >> 8;  // thread within its K group, the group
+  auto &As = As_all[grp];
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
   const int n0 = blockIdx.x * BN;
@@ -488,17 +493,55 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   const int last_tile = (p.N - 1) / TILE_N;
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
   const int m0 = blockIdx.y * BM;
-  const int ks_begin = blockIdx.z * p.ksteps_per_split;
-  const int ks_end = min(ks_begin + p.ksteps_per_split, p.KS);
+  const int wg_begin = blockIdx.z * p.ksteps_per_split;
+  const int wg_end = min(wg_begin + p.ksteps_per_split, p.KS);
+  const int part = (max(wg_end - wg_begin, 0) + KG - 1) / KG;  // steps per K group (the last may have fewer)
+  const int ks_begin = wg_begin + grp * part;
+  const int ks_end = min(ks_begin + part, wg_end);
   const int nsteps = max(ks_end - ks_begin, 0);
 
   constexpr int A_CHUNKS = BM * 4;  // 16-byte chunks of an activation tile (a multiple of 256)
   constexpr int A_PER_THREAD = A_CHUNKS / 256;
-  const uint16_t *src_row[A_PER_THREAD];
+  // Addressing: a uniform base per step (scalar registers) plus a lane
+  // offset fixed for the kernel (32 bits), so a step's loads cost no vector
+  // address arithmetic (64-bit per-lane index math per step measured ~300 of
+  // ~1200 cycles per step on RTN M=512).
+  const char *a_blk = reinterpret_cast<const char *>(a + static_cast<int64_t>(m0) * p.lda);
+  uint32_t a_off[A_PER_THREAD];
 #pragma unroll
   for (int i = 0; i < A_PER_THREAD; ++i) {
     const int ch = tid + 256 * i;
-    src_row[i] = a + static_cast<int64_t>(min(m0 + (ch >> 2), p.M - 1)) * p.lda + 8 * (ch & 3);
+    a_off[i] = static_cast<uint32_t>((min(m0 + (ch >> 2), p.M - 1) - m0) * p.lda * 2 + 16 * (ch & 3));
+  }
+  // Weight, scale and zero lane offsets per column tile j (bytes; RTN scale
+  // and zero ones in elements), and the tile's first 16-column tile.
+  constexpr bool ROWS = fmt_rows(FMT);  // RTN / DSV4: one byte row per output column
+  uint32_t q_off[WN], s_off[WN], z_off[WN];
+  int tl_of[WN];
+#pragma unroll
+  for (int j = 0; j < WN; ++j) {
+    const int tl = min(tw + j, last_tile);
+    tl_of[j] = tl;
+    // Clamped like the RTN scale/zero rows: with N % 16 == 8 the upper lanes
+    // of the last tile name rows past the weight (their results are unused).
+    const int n = min(TILE_N * tl + c16, p.N - 1);
+    if constexpr (FMT == FMT_GPTQ) {
+      q_off[j] = static_cast<uint32_t>(c16 * 16 + quad * 4);
+      s_off[j] = static_cast<uint32_t>(c16 * 2);
+      z_off[j] = static_cast<uint32_t>((c16 >> 3) * 4);
+    } else if constexpr (FMT == FMT_GPTQ8) {
+      q_off[j] = static_cast<uint32_t>(c16 * 32 + quad * 8);
+      s_off[j] = static_cast<uint32_t>(c16 * 2);
+      z_off[j] = static_cast<uint32_t>((c16 >> 2) * 4);
+    } else if constexpr (FMT == FMT_RTN_T) {
+      q_off[j] = static_cast<uint32_t>(n * p.row_bytes + 4 * quad);
+      s_off[j] = static_cast<uint32_t>((n / p.rtn_gs) * p.K_logical + 8 * quad);  // elements
+      z_off[j] = s_off[j];
+    } else {
+      q_off[j] = static_cast<uint32_t>(n * p.row_bytes + (FMT == FMT_DSV4_2 ? 2 : 4) * quad);
+      s_off[j] = static_cast<uint32_t>(n * p.sz_stride_n);  // elements
+      z_off[j] = s_off[j];
+    }
   }
   // Stage registers: per step in flight, the activation chunks, weight
   // words and group parameters (GPTQ: scale bits and zero word; RTN: scale
@@ -508,12 +551,16 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   uint32_t sq[PF][WN], ss[PF][WN], sz[PF][WN];
   uint32_t sq8[PF][WN];  // 8-bit: the second word of the lane's 8 codes
   uint32_t sst[PF][WN][4], szt[PF][WN][4];  // RTN_T: the 8 K rows' scales / zeros (16-bit pairs)
+  const char *qb = static_cast<const char *>(p.qw);
+  const char *sb = static_cast<const char *>(p.scales);
+  const char *zb = static_cast<const char *>(p.zeros);
   auto load = [&](auto fc, int ks) __attribute__((always_inline)) {
     constexpr int f = decltype(fc)::value;
     ks = min(ks, max(ks_end - 1, 0));
+    const char *ab = a_blk + 64 * static_cast<int64_t>(ks);
 #pragma unroll
     for (int i = 0; i < A_PER_THREAD; ++i) {
-      const uint4 v = *reinterpret_cast<const uint4 *>(src_row[i] + 32 * ks);
+      const uint4 v = *reinterpret_cast<const uint4 *>(ab + a_off[i]);
       sa[f][4 * i] = v.x;
       sa[f][4 * i + 1] = v.y;
       sa[f][4 * i + 2] = v.z;
@@ -521,40 +568,42 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
     }
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
-      const int tl = min(tw + j, last_tile);
+      const int tl = tl_of[j];
       if constexpr (FMT == FMT_GPTQ8) {
         // Codes of K rows 8 quad .. 8 quad + 7: words 2 quad, 2 quad + 1.
-        const uint2 v = *reinterpret_cast<const uint2 *>(
-            static_cast<const uint32_t *>(p.qw) + ((static_cast<int64_t>(tl) * p.KS + ks) * TILE_N + c16) * 8 +
-            2 * quad);
+        const uint2 v = *reinterpret_cast<const uint2 *>(qb + (static_cast<int64_t>(tl) * p.KS + ks) * 512 + q_off[j]);
         sq[f][j] = v.x;
         sq8[f][j] = v.y;
         const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
-        ss[f][j] = static_cast<const uint16_t *>(p.scales)[tgs * TILE_N + c16];
-        sz[f][j] = static_cast<const uint32_t *>(p.zeros)[tgs * 4 + (c16 >> 2)];
-        continue;
-      }
-      sq[f][j] = load_word<FMT>(p, p.qw, tl, ks, quad, c16);
-      if constexpr (FMT == FMT_RTN_T) {
+        ss[f][j] = *reinterpret_cast<const uint16_t *>(sb + tgs * 32 + s_off[j]);
+        sz[f][j] = *reinterpret_cast<const uint32_t *>(zb + tgs * 16 + z_off[j]);
+      } else if constexpr (FMT == FMT_GPTQ) {
+        sq[f][j] = *reinterpret_cast<const uint32_t *>(qb + (static_cast<int64_t>(tl) * p.KS + ks) * 256 + q_off[j]);
+        const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
+        ss[f][j] = *reinterpret_cast<const uint16_t *>(sb + tgs * 32 + s_off[j]);
+        sz[f][j] = *reinterpret_cast<const uint32_t *>(zb + tgs * 8 + z_off[j]);
+      } else if constexpr (FMT == FMT_RTN_T) {
+        sq[f][j] = *reinterpret_cast<const uint32_t *>(qb + 16 * static_cast<int64_t>(ks) + q_off[j]);
         // Scales / zeros of K rows 32 ks + 8 quad .. +7 in the group of column n.
-        const int n = min(TILE_N * tl + c16, p.N - 1);
-        const int64_t i = static_cast<int64_t>(n / p.rtn_gs) * p.K_logical + 32 * ks + 8 * quad;
-        const uint4 sv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.scales) + i);
-        const uint4 zv = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(p.zeros) + i);
+        const uint4 sv = *reinterpret_cast<const uint4 *>(sb + 64 * static_cast<int64_t>(ks) + 2 * s_off[j]);
+        const uint4 zv = *reinterpret_cast<const uint4 *>(zb + 64 * static_cast<int64_t>(ks) + 2 * z_off[j]);
         sst[f][j][0] = sv.x; sst[f][j][1] = sv.y; sst[f][j][2] = sv.z; sst[f][j][3] = sv.w;
         szt[f][j][0] = zv.x; szt[f][j][1] = zv.y; szt[f][j][2] = zv.z; szt[f][j][3] = zv.w;
-        continue;
-      }
-      if constexpr (FMT == FMT_GPTQ) {
-        const int64_t tgs = static_cast<int64_t>(tl) * p.G + group_of(p, ks);
-        ss[f][j] = static_cast<const uint16_t *>(p.scales)[tgs * TILE_N + c16];
-        sz[f][j] = static_cast<const uint32_t *>(p.zeros)[tgs * 2 + (c16 >> 3)];
       } else {
-        const int n = min(TILE_N * tl + c16, p.N - 1);
-        const int64_t i = static_cast<int64_t>(n) * p.sz_stride_n + ((32 * ks + 8 * quad) / p.rtn_gs) * p.sz_stride_g;
+        if constexpr (FMT == FMT_DSV4_2)  // 8 two-bit codes: 2 bytes
+          sq[f][j] = *reinterpret_cast<const uint16_t *>(qb + 8 * static_cast<int64_t>(ks) + q_off[j]);
+        else
+          sq[f][j] = *reinterpret_cast<const uint32_t *>(qb + 16 * static_cast<int64_t>(ks) + q_off[j]);
+        // The group of K rows 32 ks + 8 quad .. + 7: a multiply-high by the
+        // launch's reciprocal (exact for this layer's offsets), else a division.
+        const uint32_t x = static_cast<uint32_t>(32 * ks + 8 * quad);
+        uint32_t g;
+        if (p.rtn_gs_magic != 0) g = __umulhi(x, p.rtn_gs_magic);
+        else g = x / static_cast<uint32_t>(p.rtn_gs);
+        const uint32_t i = s_off[j] + g * static_cast<uint32_t>(p.sz_stride_g);
         if constexpr (RDT != 0) {
-          ss[f][j] = static_cast<const uint16_t *>(p.scales)[i];
-          sz[f][j] = static_cast<const uint16_t *>(p.zeros)[i];
+          ss[f][j] = *reinterpret_cast<const uint16_t *>(sb + 2 * i);
+          sz[f][j] = *reinterpret_cast<const uint16_t *>(zb + 2 * i);
         } else {
           ss[f][j] = __float_as_uint(load_any_f32(p.scales, i, p.scale_dtype));
           sz[f][j] = __float_as_uint(load_any_f32(p.zeros, i, p.zero_dtype));
@@ -582,15 +631,41 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
   for (int t = 0; t < WM; ++t)
 #pragma unroll
     for (int j = 0; j < WN; ++j) acc[t][j] = v4f32{0.f, 0.f, 0.f, 0.f};
+  // RTN (16-bit activations): the exact single-rounding dequant when every
+  // group parameter this workgroup reads allows it (checked once, the loads
+  // overlapping the prologue's; the loop is built for both cases).
+  constexpr bool RTN16 = FMT == FMT_RTN && DT != OC_DTYPE_F32;
+  bool fast = false;
+  if constexpr (RTN16) {
+    const int k_lo = 32 * wg_begin, k_hi = 32 * max(wg_end, wg_begin + 1) - 1;
+    const int g0 = k_lo / p.rtn_gs, ng = k_hi / p.rtn_gs - g0 + 1;
+    bool ok = true;
+    for (int i = tid; i < BN * ng; i += 256) {
+      const int n = min(n0 + i / ng, p.N - 1);
+      const int64_t e = n * p.sz_stride_n + static_cast<int64_t>(g0 + i % ng) * p.sz_stride_g;
+      RtnParam rp;
+      rp.sq = round_to<DT>(load_any_f32(p.scales, e, p.scale_dtype));
+      rp.zq = round_to<DT>(load_any_f32(p.zeros, e, p.zero_dtype));
+      ok = ok && rtn_fast_ok<DT>(rp);
+    }
+    fast = __syncthreads_and(ok) != 0;
+  }
   if (nsteps > 0) store_a(0, ic<0>{});
   barrier_no_fence();
 
-  const int nsteps_pad = (nsteps + PF - 1) / PF * PF;
+  const int nsteps_pad = (part + PF - 1) / PF * PF;  // the same in every group (one barrier per step)
+  auto main_loop = [&](auto fastc) __attribute__((always_inline)) {
+  constexpr bool FAST = decltype(fastc)::value;
   for (int i0 = 0; i0 < nsteps_pad; i0 += PF) {
     static_for<0, PF>([&](auto fc) __attribute__((always_inline)) {
       constexpr int f = decltype(fc)::value;
       const int i = i0 + f;  // step ks_begin + i sits in stage f; refilled once consumed
       if (i < nsteps) {      // uniform over the workgroup
+        // A fragments first: their LDS latency overlaps the dequantization.
+        uint4 av[WM];
+#pragma unroll
+        for (int t = 0; t < WM; ++t)
+          av[t] = *reinterpret_cast<const uint4 *>(&As[i & 1][(16 * t + c16) * A_LDS_STRIDE + 8 * quad]);
         uint4 b[WN];
 #pragma unroll
         for (int j = 0; j < WN; ++j) {
@@ -629,22 +704,46 @@ __global__ __launch_bounds__(256) void gemm_tiled_kernel(GemmParams p) {
               rp.sq = round_to<DT>(__uint_as_float(ss[f][j]));
               rp.zq = round_to<DT>(__uint_as_float(sz[f][j]));
             }
-            b[j] = rtn_dequant8<DT>(sq[f][j], rp);
+            if constexpr (FAST) b[j] = rtn_dequant8_fast<DT>(sq[f][j], rp);
+            else b[j] = rtn_dequant8<DT>(sq[f][j], rp);
           }
         }
 #pragma unroll
-        for (int t = 0; t < WM; ++t) {
-          const uint4 av = *reinterpret_cast<const uint4 *>(&As[i & 1][(16 * t + c16) * A_LDS_STRIDE + 8 * quad]);
+        for (int t = 0; t < WM; ++t)
 #pragma unroll
-          for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av, b[j], acc[t][j]);
-        }
+          for (int j = 0; j < WN; ++j) acc[t][j] = mfma16x16x32<DT>(av[t], b[j], acc[t][j]);
         if (i + 1 < nsteps) store_a((i + 1) & 1, ic<(f + 1) % PF>{});
       }
       load(fc, ks_begin + i + PF);
       barrier_no_fence();  // the next step's activations are in LDS; this step's reads are done
     });
   }
+  };
+  if (RTN16 && fast) main_loop(std::true_type{});
+  else main_loop(std::false_type{});
 
+  if constexpr (KG > 1) {
+    // Groups 1.. park their sums; group 0 adds them in group order.
+    __shared__ float red[KG > 1 ? (KG - 1) * BM * BN : 1];
+    auto slot = [&](int g, int t, int j, int i) { return (((g * 4 + wave) * WM + t) * WN * 4 + j * 4 + i) * 64 + lane; };
+    if (grp > 0) {
+#pragma unroll
+      for (int t = 0; t < WM; ++t)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) red[slot(grp - 1, t, j, i)] = acc[t][j][i];
+    }
+    __syncthreads();
+    if (grp > 0) return;
+    for (int g = 0; g < KG - 1; ++g)
+#pragma unroll
+      for (int t = 0; t < WM; ++t)
+#pragma unroll
+        for (int j = 0; j < WN; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t][j][i] += red[slot(g, t, j, i)];
+  }
   // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
   if (p.ksplit == 1 && !p.out_f32) {
 #pragma unroll
@@ -1074,8 +1173,46 @@ __global__ __launch_bounds__(ROUTE_THREADS) void moe_route_kernel(const int64_t 
 // Host dispatch.
 
 struct TileCfg {
-  int wm, wn;
+  int wm, wn, kg;
 };
+
+// Shape of the LDS-tiled kernel: the largest tile whose grid fills the chip
+// (want workgroups, one per CU), else 64 x 64 tiles. Those run K groups: two
+// when their grid fills the chip, four (no K split) from half of it, and a
+// K split over fp32 partials below that (each part of 16 or more steps when
+// split_k allows it). Measured on MI355X, 64 x 64 tiles: RTN M=512 K=1024
+// N=2048 (256 tiles) 15.1 / 12.5 / 13.2 us with 1 / 2 / 4 groups; padded
+// gs26 M=256 K=1056 N=3072 (192 tiles) 18.9 us split in two, 15.0 us with
+// four groups and no split.
+int env_int(const char *name, int dflt);
+TileCfg pick_tiles(int M, int N, int ksteps, int *ksplit, int *ksteps_per_split, bool split_k = true) {
+  static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
+  static const TileCfg cfgs[] = {{16, 3, 1}, {8, 2, 1}, {4, 1, 1}};
+  TileCfg pick = cfgs[2];
+  for (const TileCfg &c : cfgs) {
+    if (static_cast<int64_t>((M + 16 * c.wm - 1) / (16 * c.wm)) * ((N + 64 * c.wn - 1) / (64 * c.wn)) >= want) {
+      pick = c;
+      break;
+    }
+  }
+  const int64_t tiles = static_cast<int64_t>((M + 16 * pick.wm - 1) / (16 * pick.wm)) *
+                        ((N + 64 * pick.wn - 1) / (64 * pick.wn));
+  int ks = 1;
+  if (pick.wm == 4) {
+    if (tiles >= want) {
+      pick.kg = ksteps >= 16 ? 2 : 1;
+    } else if (2 * tiles >= want || !split_k) {
+      pick.kg = ksteps >= 32 ? 4 : ksteps >= 16 ? 2 : 1;
+    } else {
+      ks = static_cast<int>(std::min<int64_t>(want / tiles, std::max(1, ksteps / 16)));
+      const int per = (ksteps + ks - 1) / ks;
+      pick.kg = per >= 32 ? 4 : per >= 16 ? 2 : 1;
+    }
+  }
+  *ksteps_per_split = (ksteps + ks - 1) / ks;
+  *ksplit = (ksteps + *ksteps_per_split - 1) / *ksteps_per_split;
+  return pick;
+}
 
 int env_int(const char *name, int dflt) {
   const char *v = std::getenv(name);
@@ -1268,22 +1405,7 @@ Plan plan_gemm(int M, int N, int K_phys, int group_rows, bool has_kmap, int regi
     sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
     return sp;
   }
-  static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
-  TileCfg pick = cfgs[2];
-  for (const TileCfg &c : cfgs) {
-    const int64_t tiles = static_cast<int64_t>((M + 16 * c.wm - 1) / (16 * c.wm)) *
-                          ((N + 64 * c.wn - 1) / (64 * c.wn));
-    if (tiles >= want) {
-      pick = c;
-      break;
-    }
-  }
-  sp.tile = pick;
-  const int tiles = ((M + 16 * pick.wm - 1) / (16 * pick.wm)) * ((N + 64 * pick.wn - 1) / (64 * pick.wn));
-  int ksplit = 1;
-  if (tiles < want) ksplit = std::min((want + tiles - 1) / tiles, std::max(1, ksteps / 8));
-  sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
-  sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
+  sp.tile = pick_tiles(M, N, ksteps, &sp.ksplit, &sp.ksteps_per_split);
   return sp;
 }
 
@@ -1365,18 +1487,28 @@ void launch_mfma(const GemmParams &p, int mt, hipStream_t s) {
   }
 }
 
-template <int DT, int SDT, int WM, int WN, int FMT>
-void launch_tiled_t(const GemmParams &p, hipStream_t s) {
+// ceil(2^32 / gs) when x * gs < 2^32 for every offset x < K (then
+// umulhi(x, magic) = floor(x / gs): the error x (magic - 2^32 / gs) / 2^32 is
+// below x / 2^32 < 1 / gs), else 0.
+static uint32_t group_magic(int gs, int K) {
+  if (gs < 2 || static_cast<uint64_t>(K) * static_cast<uint64_t>(gs) >= (uint64_t{1} << 32)) return 0;
+  return static_cast<uint32_t>(((uint64_t{1} << 32) + gs - 1) / gs);
+}
+
+template <int DT, int SDT, int WM, int WN, int FMT, int KG>
+void launch_tiled_t(const GemmParams &p_in, hipStream_t s) {
+  GemmParams p = p_in;
+  p.rtn_gs_magic = fmt_rows(FMT) ? group_magic(p.rtn_gs, p.K_phys) : 0;
   const dim3 grid((p.N + 64 * WN - 1) / (64 * WN), (p.M + 16 * WM - 1) / (16 * WM), p.ksplit);
   const bool same16 = fmt_rows(FMT) && p.scale_dtype == p.zero_dtype;
   if (same16 && p.scale_dtype == OC_DTYPE_F16)
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_F16 : 0>), grid, dim3(256),
-                       0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_F16 : 0, KG>), grid,
+                       dim3(256 * KG), 0, s, p);
   else if (same16 && p.scale_dtype == OC_DTYPE_BF16)
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_BF16 : 0>), grid, dim3(256),
-                       0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, fmt_rows(FMT) ? OC_DTYPE_BF16 : 0, KG>), grid,
+                       dim3(256 * KG), 0, s, p);
   else
-    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0>), grid, dim3(256), 0, s, p);
+    hipLaunchKernelGGL((gemm_tiled_kernel<DT, SDT, WM, WN, FMT, 0, KG>), grid, dim3(256 * KG), 0, s, p);
   if (p.ksplit > 1 && !p.out_f32) {
     const int64_t mn = static_cast<int64_t>(p.M) * p.N;
     hipLaunchKernelGGL(splitk_reduce_kernel<DT>, dim3(static_cast<unsigned>((mn / 4 + 255) / 256)), dim3(256), 0,
@@ -1386,9 +1518,11 @@ void launch_tiled_t(const GemmParams &p, hipStream_t s) {
 
 template <int DT, int SDT, int FMT>
 void launch_tiled(const GemmParams &p, TileCfg c, hipStream_t s) {
-  if (c.wm == 16 && c.wn == 3) launch_tiled_t<DT, SDT, 16, 3, FMT>(p, s);
-  else if (c.wm == 8 && c.wn == 2) launch_tiled_t<DT, SDT, 8, 2, FMT>(p, s);
-  else launch_tiled_t<DT, SDT, 4, 1, FMT>(p, s);
+  if (c.wm == 16 && c.wn == 3) launch_tiled_t<DT, SDT, 16, 3, FMT, 1>(p, s);
+  else if (c.wm == 8 && c.wn == 2) launch_tiled_t<DT, SDT, 8, 2, FMT, 1>(p, s);
+  else if (c.kg == 4) launch_tiled_t<DT, SDT, 4, 1, FMT, 4>(p, s);
+  else if (c.kg == 2) launch_tiled_t<DT, SDT, 4, 1, FMT, 2>(p, s);
+  else launch_tiled_t<DT, SDT, 4, 1, FMT, 1>(p, s);
 }
 
 // Launch shape: 128 x 192 tiles, one K step per stage (4-deep ring). Measured
@@ -1435,36 +1569,22 @@ void launch_gptq(const GemmParams &p, const Plan &sp, hipStream_t s) {
 Plan plan_tiled_only(int M, int N, int K_phys, bool has_kmap) {
   Plan sp{};
   sp.regime = OC_REGIME_TILED;
-  const int ksteps = K_phys / 32;
-  static const int want = std::max(1, env_int("ONECOMP_HIP_TILED_MIN_WGS", 256));
-  static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
-  TileCfg pick = cfgs[2];
-  for (const TileCfg &c : cfgs) {
-    if (static_cast<int64_t>((M + 16 * c.wm - 1) / (16 * c.wm)) * ((N + 64 * c.wn - 1) / (64 * c.wn)) >= want) {
-      pick = c;
-      break;
-    }
-  }
-  sp.tile = pick;
-  const int tiles = ((M + 16 * pick.wm - 1) / (16 * pick.wm)) * ((N + 64 * pick.wn - 1) / (64 * pick.wn));
-  int ksplit = 1;
-  if (tiles < want) ksplit = std::min((want + tiles - 1) / tiles, std::max(1, ksteps / 8));
-  sp.ksteps_per_split = (ksteps + ksplit - 1) / ksplit;
-  sp.ksplit = (ksteps + sp.ksteps_per_split - 1) / sp.ksteps_per_split;
+  sp.tile = pick_tiles(M, N, K_phys / 32, &sp.ksplit, &sp.ksteps_per_split);
   sp.gather = has_kmap;
   return sp;
 }
 
-void plan_tiled(int M, int N, int K, int *wm, int *wn, int *ksplit, int *ksteps_per_split) {
+void plan_tiled(int M, int N, int K, int *wm, int *wn, int *kg, int *ksplit, int *ksteps_per_split) {
   const Plan sp = plan_tiled_only(M, N, K, false);
   *wm = sp.tile.wm;
   *wn = sp.tile.wn;
+  *kg = sp.tile.kg;
   *ksplit = sp.ksplit;
   *ksteps_per_split = sp.ksteps_per_split;
 }
 
-void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, hipStream_t s) {
-  const TileCfg c{wm, wn};
+void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, int kg, hipStream_t s) {
+  const TileCfg c{wm, wn, kg};
   const bool bf = x_dtype == OC_DTYPE_BF16;
   if (transposed) {
     if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN_T>(p, c, s);
@@ -1776,14 +1896,8 @@ int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_
 
   // Bias is rounded to the activation type first (`bias.to(x.dtype)`); the
   // kernel adds it in fp32, which is exact for a 16-bit value.
-  static const TileCfg cfgs[] = {{16, 3}, {8, 2}, {4, 1}};
-  TileCfg pick = cfgs[2];
-  for (const TileCfg &t : cfgs) {
-    if (static_cast<int64_t>((M + 16 * t.wm - 1) / (16 * t.wm)) * ((N + 64 * t.wn - 1) / (64 * t.wn)) >= 256) {
-      pick = t;
-      break;
-    }
-  }
+  int rtn_ksplit = 1, rtn_kps = K / 32;  // no K split: the layer writes its output directly
+  const TileCfg pick = pick_tiles(M, N, K / 32, &rtn_ksplit, &rtn_kps, false);
   GemmParams p{};
   p.a = x;
   p.lda = ldx;

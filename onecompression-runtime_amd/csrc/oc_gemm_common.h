@@ -35,6 +35,8 @@ struct GemmParams {
   int scale_dtype;     // RTN (runtime)
   int zero_dtype;      // RTN (runtime)
   int rtn_gs;          // RTN / DSV4: columns per group
+  uint32_t rtn_gs_magic;  // ceil(2^32 / rtn_gs) when floor(x / rtn_gs) = umulhi(x, magic) for every
+                          // K offset x of the layer, else 0 (set by the tiled launch)
   int rtn_G;           // RTN: groups per row
   int row_bytes;       // RTN / DSV4
   int64_t sz_stride_n;  // RTN / DSV4: scale/zero element offset per output row ...
@@ -203,8 +205,8 @@ int env_int(const char *name, int dflt);
 // for an M x N x K problem, and a launch of FMT_RTN (transposed = false) or
 // FMT_RTN_T. With p.out_f32 (or a K split) the kernel writes fp32 partials
 // [ksplit][M][N] to p.partials and nothing else.
-void plan_tiled(int M, int N, int K, int *wm, int *wn, int *ksplit, int *ksteps_per_split);
-void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, hipStream_t s);
+void plan_tiled(int M, int N, int K, int *wm, int *wn, int *kg, int *ksplit, int *ksteps_per_split);
+void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, int kg, hipStream_t s);
 
 // Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
 // ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.

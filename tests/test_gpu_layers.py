@@ -48,6 +48,39 @@ def test_rtn_linear_one_hot_bit_exact(M, G):
     assert np.array_equal(bits16(out), oracle_bits(wd[:, ks].T, torch.bfloat16))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M", [7, 200])
+def test_rtn_linear_exact_shortcut_and_general_groups(dtype, M):
+    """Integral zeros (|z| <= 240) with positive scales take the kernel's
+    single-rounding shortcut; fractional or large zeros and zero or negative
+    scales the per-op path. Both within one layer (mixed per wave and per
+    step), one-hot inputs: bit-exact against the per-op-rounded oracle
+    (+ 0.0: a GEMM output carries no negative zero)."""
+    from onecomp_runtime import PackedRTNLinear
+
+    rng = np.random.default_rng(31 + M)
+    K, N, G = 256, 96, 4
+    q = rng.integers(0, 256, (N, K // 2)).astype(np.uint8)
+    s = (np.abs(rng.standard_normal((N, G))) * 0.05 + 1e-3).astype(np.float16)
+    z = rng.integers(0, 16, (N, G)).astype(np.float16)
+    z[0:16, 1] = 240.0        # shortcut bound
+    z[16:32, 2] = -240.0
+    z[32, 0] = 241.0          # past the bound: per-op path for that wave's step
+    z[40, 3] = 7.5            # fractional
+    z[48:64, :] = 300.0       # large: RNE(c - z) rounds in bf16
+    s[64, 1] = -0.02          # negative scale
+    s[80, 2] = 0.0            # zero scale
+    mod = PackedRTNLinear(K, N, torch.from_numpy(q).to(DEV), torch.from_numpy(s).to(DEV),
+                          torch.from_numpy(z).to(DEV))
+    fmt = "bf16" if dtype == torch.bfloat16 else "f16"
+    wd = O.rtn_dequant(q, s.astype(np.float32), z.astype(np.float32), K, N, fmt)
+    ks = rng.integers(0, K, M)
+    x = torch.zeros((M, K), dtype=dtype)
+    x[torch.arange(M), torch.from_numpy(ks)] = 1.0
+    say(f"rtn shortcut/general mix M={M} {dtype}")
+    assert np.array_equal(bits16(mod(x.to(DEV))), oracle_bits(wd[:, ks].T + 0.0, dtype))
+
+
 @pytest.mark.parametrize("N", [24, 40])
 @pytest.mark.parametrize("M", [1, 65, 200])
 def test_rtn_linear_ragged_tile_n(N, M):
