@@ -1,8 +1,9 @@
 """Calls on different HIP streams that overlap in time use separate GEMM
 workspaces: a decode layer whose balanced ranges cut tiles (partials swapped
-through the workspace's counter cells) and a split-K layer (fp32 partials
-and gathered activations in the workspace) run concurrently, many times, on
-two streams; every output equals the single-stream result bit for bit and
+through the workspace's counter cells) and a split-K act-order layer (fp32
+partials, and activation rows gathered into the workspace: K beyond what the
+tiled kernel gathers in its loads) run concurrently, many times, on two
+streams; every output equals the single-stream result bit for bit and
 matches the oracle."""
 import pytest
 import torch
@@ -16,21 +17,21 @@ DEV = "cuda:0"
 
 def test_two_streams_overlapping_calls():
     from onecomp_runtime import kernels, synthetic
-    from onecomp_runtime.layers import FusedInt4LinearPaddedGroups, PackedGPTQLinear
+    from onecomp_runtime.layers import PackedGPTQLinear
 
     dec = synthetic.gptq_layer(5120, 17408, seed=20500, act_order=True)
-    pad = synthetic.gptq_layer(1040, 3072, seed=20501, groupsize=26, pad_rows_to=1056)
+    sk = synthetic.gptq_layer(9216, 2048, seed=20501, act_order=True)
     a = PackedGPTQLinear(5120, 17408, dec.qweight.to(DEV), dec.scales.to(DEV), dec.qzeros.to(DEV),
                          g_idx=dec.g_idx.to(DEV), groupsize=32)
-    b = FusedInt4LinearPaddedGroups(1040, 3072, pad.qweight.to(DEV), pad.scales.to(DEV), pad.qzeros.to(DEV),
-                                    groupsize=26)
+    b = PackedGPTQLinear(9216, 2048, sk.qweight.to(DEV), sk.scales.to(DEV), sk.qzeros.to(DEV),
+                         g_idx=sk.g_idx.to(DEV), groupsize=32)
     xa = synthetic.activations(1, 5120, seed=20502).to(DEV)
-    xb = synthetic.activations(256, 1040, seed=20503).to(DEV)
-    # the decode call uses the counter cells, the padded one split-K partials
+    xb = synthetic.activations(96, 9216, seed=20503).to(DEV)
+    # the decode call uses the counter cells, the act-order one gathered rows and split-K partials
     from onecomp_runtime import _hip
 
     assert _hip.gemm_workspace_bytes(1, 17408, a.k_phys, a.group_rows, True, 0) > 0
-    assert _hip.gemm_workspace_bytes(256, 3072, b.k_phys, b.group_rows, True, 0) > 512 * 1024
+    assert _hip.gemm_workspace_bytes(96, 2048, b.k_phys, b.group_rows, True, 0) > 512 * 1024 + 96 * 9216 * 2
     say("two streams: single-stream references")
     with torch.no_grad():
         ref_a, ref_b = a(xa), b(xb)
@@ -53,4 +54,4 @@ def test_two_streams_overlapping_calls():
     keys = {k for k in _hip.workspace._bufs if k[0] == 0}
     assert {(0, s1.cuda_stream), (0, s2.cuda_stream)} <= keys
     assert_gemm_close(ref_a, O.gptq_linear(np32(xa), *layer_oracle_inputs(dec), 5120, 17408, "bf16"), "decode")
-    assert_gemm_close(ref_b, O.gptq_linear(np32(xb), *layer_oracle_inputs(pad), 1040, 3072, "bf16"), "padded")
+    assert_gemm_close(ref_b, O.gptq_linear(np32(xb), *layer_oracle_inputs(sk), 9216, 2048, "bf16"), "split-K act-order")
