@@ -209,6 +209,20 @@ def dominant_kernel(dev, built, xs, copies, iters):
             "calibration_copy_bytes": CALIB_COPY_BYTES}
 
 
+def dense_library_us(dev, M, K, N, copies=2):
+    """Context only: the same-shape GEMM on already dequantized bf16 weights as
+    the vendor library (hipBLASLt, via F.linear) runs it, weight copies
+    rotated like the packed layer's, graph replays."""
+    import torch
+
+    x = torch.randn(M, K, dtype=torch.bfloat16, device=dev)
+    ws = [torch.randn(N, K, dtype=torch.bfloat16, device=dev) for _ in range(copies)]
+    with torch.no_grad():
+        ms = graph_ms([lambda w=w: torch.nn.functional.linear(x, w) for w in ws])
+    del x, ws
+    return ms * 1e3
+
+
 def gptq_m16_workload(dev, steps, warmup):
     import torch
 
@@ -223,8 +237,10 @@ def gptq_m16_workload(dev, steps, warmup):
         ms_eager = time_ms(lambda i: mods[i % copies](x), steps * 4, warmup)
         ms = graph_ms([lambda m=m: m(x) for m in mods])
     gbps = gptq_bytes(K, N) / (ms * 1e-3) / 1e9
+    dense_copies = math.ceil(2 * MALL_BYTES / (K * N * 2))
     return {"M": 16, "K": K, "N": N, "us": ms * 1e3, "weight_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBS,
-            "TFLOPs": 2 * 16 * K * N / (ms * 1e-3) / 1e12, "us_eager": ms_eager * 1e3}
+            "TFLOPs": 2 * 16 * K * N / (ms * 1e-3) / 1e12, "us_eager": ms_eager * 1e3,
+            "dense_bf16_library_us": dense_library_us(dev, 16, K, N, dense_copies)}
 
 
 def dit_workload(dev, steps, warmup):
@@ -271,7 +287,8 @@ def padded_workload(dev, steps, warmup):
     tf = 2 * M * K * N / (ms * 1e-3) / 1e12
     wb = 1056 // 8 * N * 4 + 40 * N * 2 + 40 * N // 8 * 4
     return {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
-            "GBps": (wb + M * K * 2 + M * N * 2) / (ms * 1e-3) / 1e9, "us_eager": ms_eager * 1e3}
+            "GBps": (wb + M * K * 2 + M * N * 2) / (ms * 1e-3) / 1e9, "us_eager": ms_eager * 1e3,
+            "dense_bf16_library_us": dense_library_us(dev, M, K, N)}
 
 
 def rtn_workload(dev, steps, warmup):
@@ -289,7 +306,7 @@ def rtn_workload(dev, steps, warmup):
         ms = graph_ms([lambda: mod(x)] * 8)
     tf = 2 * M * K * N / (ms * 1e-3) / 1e12
     res["rtn_linear_m512"] = {"us": ms * 1e3, "TFLOPs": tf, "mfma_frac": tf / BF16_PEAK_TFLOPS,
-                              "us_eager": ms_eager * 1e3}
+                              "us_eager": ms_eager * 1e3, "dense_bf16_library_us": dense_library_us(dev, M, K, N)}
     V, D, T = 32768, 1024, 4096
     for G in (1, 32):
         emb_layer = synthetic.rtn_layer(V, D, seed=20310, groups=G)
