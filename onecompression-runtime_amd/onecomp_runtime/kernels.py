@@ -254,6 +254,62 @@ def int4_gemm(a_2d: torch.Tensor, w: TiledWeights, *, in_features: int,
 
 _DT = {torch.float16: _hip.OC_DTYPE_F16, torch.bfloat16: _hip.OC_DTYPE_BF16,
        torch.float32: _hip.OC_DTYPE_F32}
+
+
+class LayerCall:
+    """One layer's GEMM call with its constant arguments bound once (weights,
+    shape, row maps): the per-call work is the activation and output
+    pointers, the stream and the workspace of this batch size. Activations
+    that are not compact 16-bit rows on the layer's device take
+    ``int4_gemm`` (which validates, copies or raises)."""
+
+    __slots__ = ("w", "qt", "in_features", "kmap", "kinv", "idx", "N", "fn", "mid", "ws", "has_kmap")
+
+    def __init__(self, w: TiledWeights, in_features: int, kmap: torch.Tensor | None,
+                 kinv: torch.Tensor | None) -> None:
+        self.w, self.qt, self.in_features, self.kmap, self.kinv = w, w.qt, int(in_features), kmap, kinv
+        self.idx = w.qt.get_device()
+        self.N = w.N
+        self.has_kmap = kmap is not None
+        self.fn = _gemm_fn() if w.wbits == 4 else lib().oc_int8_gemm
+        self.mid = (self.in_features, w.qt.data_ptr(), w.st.data_ptr(), _DT[w.st.dtype], w.zt.data_ptr(), w.N,
+                    w.k_phys, w.group_rows, None if kmap is None else kmap.data_ptr(),
+                    None if kinv is None else kinv.data_ptr())
+        self.ws: dict = {}  # (M, stream) -> (workspace pointer, bytes)
+
+    def __call__(self, a_2d: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        adt = a_2d.dtype
+        M = a_2d.shape[0]
+        if ((adt is not torch.bfloat16 and adt is not torch.float16) or not a_2d.is_cuda
+                or a_2d.get_device() != self.idx or a_2d.stride(-1) != 1 or a_2d.stride(0) % 8
+                or a_2d.data_ptr() % 16 or M * a_2d.stride(0) >= 1 << 30):
+            return int4_gemm(a_2d, self.w, in_features=self.in_features, kmap=self.kmap, kinv=self.kinv,
+                             bias=bias)
+        out = torch.empty((M, self.N), dtype=adt, device=a_2d.device)
+        stream = _hip._raw_stream(self.idx)
+        key = (M, stream)
+        wsp = self.ws.get(key)
+        if wsp is None:
+            w = self.w
+            ws, nbytes = _hip.gemm_workspace(self.idx, M, self.N, w.k_phys, w.group_rows, self.has_kmap,
+                                             _hip.OC_REGIME_AUTO, stream, w.wbits)
+            wsp = (None if ws is None else ws.data_ptr(), nbytes, ws)
+            if len(self.ws) > 64:
+                self.ws.clear()
+            self.ws[key] = wsp  # (a buffer the stream outgrows later stays allocated and valid)
+        if self.w.wbits == 4:
+            status = self.fn(a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, *self.mid,
+                             None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
+                             out.data_ptr(), out.stride(0), wsp[0], wsp[1], _hip.OC_REGIME_AUTO, stream)
+        else:
+            status = self.fn(a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, *self.mid,
+                             None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
+                             out.data_ptr(), out.stride(0), wsp[0], wsp[1], stream)
+        if status:
+            check(status, f"oc_int{self.w.wbits}_gemm")
+        return out
+
+
 _GEMM_FN = None
 
 

@@ -88,6 +88,7 @@ class _HipGPTQLinear(torch.nn.Module):
                      "_src_qweight", "_src_scales", "_src_qzeros"):
             self.register_buffer(name, None, persistent=False)
         self._weights = None
+        self._call = None  # kernels.LayerCall bound to the current tiled weights
         self._configure(g_idx, qweight.device)
         # Row and group counts of the checkpoint tensors as given (the "input"
         # state layout reproduces them).
@@ -109,6 +110,7 @@ class _HipGPTQLinear(torch.nn.Module):
         # The kernels read activations through kmap (physical -> input row) and
         # kinv (input -> physical row) only when the rows moved.
         self.kmap, self.kinv = kernels.row_maps(plan, device)
+        self._call = None
 
     def _check_sources(self, qweight, scales, qzeros, physical: bool) -> None:
         if qweight.dtype != torch.int32 or qzeros.dtype != torch.int32:
@@ -137,7 +139,7 @@ class _HipGPTQLinear(torch.nn.Module):
         self._src_qweight, self._src_scales, self._src_qzeros = qweight, scales, qzeros
         self._src_physical = physical
         self.qweight_tiled = self.scales_tiled = self.zeros_tiled = None
-        self._weights = None
+        self._weights = self._call = None
         if qweight.is_cuda:
             self._prepare()
 
@@ -288,8 +290,11 @@ class _HipGPTQLinear(torch.nn.Module):
         a_2d = x.reshape(-1, self.in_features)
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
-        c = kernels.int4_gemm(a_2d, self.tiled(), in_features=self.in_features, kmap=self.kmap,
-                              kinv=self.kinv, bias=bias)
+        call, buf = self._call, self._buffers
+        if call is None or call.qt is not buf.get("qweight_tiled") or call.w.st is not buf.get("scales_tiled"):
+            w = self.tiled()
+            call = self._call = kernels.LayerCall(w, self.in_features, self.kmap, self.kinv)
+        c = call(a_2d, bias)
         out = c.reshape(*x.shape[:-1], self.out_features)
         if orig_dtype == torch.float32:
             out = out.to(torch.float32)
@@ -328,6 +333,7 @@ class _HipGPTQLinear(torch.nn.Module):
         before = {n: getattr(self, n) for n in ("qweight_tiled", "zeros_tiled", "kmap", "_src_qweight",
                                                 "_src_qzeros")}
         kinv_before = self.kinv
+        self._call = None
         result = super()._apply(fn, recurse=recurse)
         for name, old in before.items():
             new = getattr(self, name)
