@@ -310,16 +310,22 @@ def rtn_workload(dev, steps, warmup):
     V, D, T = 32768, 1024, 4096
     for G in (1, 32):
         emb_layer = synthetic.rtn_layer(V, D, seed=20310, groups=G)
-        emb = PackedEmbedding(V, D, emb_layer.qweight_u8.to(dev), emb_layer.scales.to(dev),
-                              emb_layer.zeros.to(dev))
-        ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311)).to(dev)
+        # Table copies covering twice the Infinity Cache, each with its own
+        # token ids: every call gathers rows the caches have not seen lately.
+        table_bytes = V * (D // 2 + 4 * G)
+        copies = max(2, -(-2 * MALL_BYTES // table_bytes))
+        embs = [PackedEmbedding(V, D, emb_layer.qweight_u8.to(dev), emb_layer.scales.to(dev),
+                                emb_layer.zeros.to(dev)) for _ in range(copies)]
+        idss = [torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(20311 + i)).to(dev)
+                for i in range(copies)]
         with torch.no_grad():
-            ms_eager = time_ms(lambda i: emb(ids), steps * 4, warmup)
-            ms = graph_ms([lambda: emb(ids)] * 8)
+            ms_eager = time_ms(lambda i: embs[i % copies](idss[i % copies]), steps * 4, warmup)
+            ms = graph_ms([lambda i=i: embs[i](idss[i]) for i in range(copies)])
         nbytes = T * (D // 2 + 4 * G) + T * 8 + T * D * 2
         res[f"rtn_embedding_G{G}"] = {"us": ms * 1e3, "GBps": nbytes / (ms * 1e-3) / 1e9,
                                       "hbm_frac": nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-                                      "us_eager": ms_eager * 1e3}
+                                      "us_eager": ms_eager * 1e3, "table_copies": copies}
+        del embs, idss
     return res
 
 

@@ -816,7 +816,7 @@ struct BigLayout {
 
 
 template <int DT, int SDT, int WM, int WN, int KPS, bool MOE, int NSX = (KPS == 1 ? 4 : 3)>
-__global__ __launch_bounds__(256, WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1) void gemm_big_kernel(GemmParams p) {
+__global__ __launch_bounds__(256, MOE && NSX == 4 ? 3 : (WM <= 8 && WN == 3 && NSX <= 6 ? 2 : 1)) void gemm_big_kernel(GemmParams p) {
   // WM 16-row tiles per workgroup; KPS K steps per ring stage (one barrier
   // per stage); ring depth NS. MOE: grid z = expert; the workgroup walks its
   // expert's routed rows (expert_offsets / sorted_pairs) in blocks of 16 WM.
@@ -1534,7 +1534,11 @@ constexpr int BIG_WM = 8, BIG_WN = 3, BIG_KPS = 1;
 constexpr int MOE_WM = BIG_WM;
 // Ring depth of the grouped launch: 4, as the dense one (measured on the
 // 64-expert top-8 workload: 6 stages no faster, 8 slower with one workgroup
-// per CU). ONECOMP_HIP_MOE_NS (4, 6 or 8) overrides (tuning only).
+// per CU). At depth 4 the kernel's launch bound asks for 3 waves per SIMD:
+// the compiler does not reach it (191 registers, 2 workgroups per CU) but the
+// schedule it makes for that target measured 217 -> 168 us on the workload;
+// a hard cap at 168 registers (3 workgroups per CU, a small spill) measured
+// the same. ONECOMP_HIP_MOE_NS (4, 6 or 8) overrides (tuning only).
 constexpr int MOE_NS = 4;
 
 template <int DT, int SDT>
