@@ -16,6 +16,11 @@ import torch
 from . import _hip
 from ._hip import check, dtype_code, lib, ptr, require_device, stream_of
 
+try:  # CPython binding of the per-layer GEMM call (built beside the library)
+    from . import _occall
+except ImportError:
+    _occall = None
+
 
 @dataclass(frozen=True)
 class GroupPlan:
@@ -259,11 +264,13 @@ _DT = {torch.float16: _hip.OC_DTYPE_F16, torch.bfloat16: _hip.OC_DTYPE_BF16,
 class LayerCall:
     """One layer's GEMM call with its constant arguments bound once (weights,
     shape, row maps): the per-call work is the activation and output
-    pointers, the stream and the workspace of this batch size. Activations
-    that are not compact 16-bit rows on the layer's device take
-    ``int4_gemm`` (which validates, copies or raises)."""
+    pointers, the stream and the workspace of this batch size. The call goes
+    through the CPython binding ``_occall.Layer`` when it is built (else
+    through ctypes, the same entry point). Activations that are not compact
+    16-bit rows on the layer's device take ``int4_gemm`` (which validates,
+    copies or raises)."""
 
-    __slots__ = ("w", "qt", "in_features", "kmap", "kinv", "idx", "N", "fn", "mid", "ws", "has_kmap")
+    __slots__ = ("w", "qt", "in_features", "kmap", "kinv", "idx", "N", "fn", "mid", "ws", "has_kmap", "h")
 
     def __init__(self, w: TiledWeights, in_features: int, kmap: torch.Tensor | None,
                  kinv: torch.Tensor | None) -> None:
@@ -276,6 +283,9 @@ class LayerCall:
                     w.k_phys, w.group_rows, None if kmap is None else kmap.data_ptr(),
                     None if kinv is None else kinv.data_ptr())
         self.ws: dict = {}  # (M, stream) -> (workspace pointer, bytes)
+        self.h = None
+        if _occall is not None:
+            self.h = _occall.Layer(ctypes.cast(self.fn, ctypes.c_void_p).value, w.wbits, *self.mid)
 
     def __call__(self, a_2d: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         adt = a_2d.dtype
@@ -297,7 +307,11 @@ class LayerCall:
             if len(self.ws) > 64:
                 self.ws.clear()
             self.ws[key] = wsp  # (a buffer the stream outgrows later stays allocated and valid)
-        if self.w.wbits == 4:
+        h = self.h
+        if h is not None:
+            status = h(a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, None if bias is None else bias.data_ptr(),
+                       0 if bias is None else _DT[bias.dtype], out.data_ptr(), out.stride(0), wsp[0], wsp[1], stream)
+        elif self.w.wbits == 4:
             status = self.fn(a_2d.data_ptr(), a_2d.stride(0), _DT[adt], M, *self.mid,
                              None if bias is None else bias.data_ptr(), 0 if bias is None else _DT[bias.dtype],
                              out.data_ptr(), out.stride(0), wsp[0], wsp[1], _hip.OC_REGIME_AUTO, stream)

@@ -287,7 +287,8 @@ class _HipGPTQLinear(torch.nn.Module):
             # fp32 input is computed in fp16 and returned as fp32
             # (fused_int4_linear.py:415-419, :535-536).
             x = x.to(torch.float16)
-        a_2d = x.reshape(-1, self.in_features)
+        flat = x.dim() == 2 and x.shape[1] == self.in_features  # rows already: no view ops
+        a_2d = x if flat else x.reshape(-1, self.in_features)
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
         call, buf = self._call, self._buffers
@@ -295,7 +296,7 @@ class _HipGPTQLinear(torch.nn.Module):
             w = self.tiled()
             call = self._call = kernels.LayerCall(w, self.in_features, self.kmap, self.kinv)
         c = call(a_2d, bias)
-        out = c.reshape(*x.shape[:-1], self.out_features)
+        out = c if flat else c.reshape(*x.shape[:-1], self.out_features)
         if orig_dtype == torch.float32:
             out = out.to(torch.float32)
         return out

@@ -31,6 +31,23 @@ def test_library_exports_every_declared_symbol():
     assert set(names) == set(_hip.SIGNATURES), set(names) ^ set(_hip.SIGNATURES)
 
 
+def test_layer_call_binding_loads_and_validates():
+    """The CPython binding of the per-layer GEMM call is built beside the
+    library and rejects bad bindings and calls before reaching the device."""
+    from onecomp_runtime import _hip, _occall
+
+    fn = ctypes.cast(_hip.lib().oc_int4_gemm, ctypes.c_void_p).value
+    with pytest.raises(ValueError):
+        _occall.Layer(0, 4, 64, None, None, 0, None, 16, 64, 32, None, None)  # no entry point
+    with pytest.raises(ValueError):
+        _occall.Layer(fn, 3, 64, None, None, 0, None, 16, 64, 32, None, None)  # wbits
+    h = _occall.Layer(fn, 4, 64, None, None, 0, None, 16, 64, 32, None, None)
+    with pytest.raises(TypeError):
+        h(0, 64, 1, 1)  # eleven arguments
+    with pytest.raises(ValueError):
+        h(0, 64, 1, -1, None, 0, 0, 16, None, 0, 0)  # negative M, refused before the call
+
+
 def test_status_strings_and_version():
     from onecomp_runtime import _hip
 
