@@ -357,6 +357,90 @@ def moe_workload(dev, steps, warmup):
             "us_eager": ms_eager * 1e3}
 
 
+PCIE_H2D_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def next_rows_workload(dev, steps, warmup):
+    """The rows after the hot path, measured the same way: GPTQ groupsize 128
+    in 4 and 8 bits (Qwen-style K=N=5120) at M=1 and 16; DSV4 int4 / int2
+    gs128 K=7168 N=2048 at M=1, device-resident and as host-resident routed
+    experts (pinned copies per call); packed Conv1d / ConvTranspose1d."""
+    import torch
+
+    from onecomp_runtime import PackedGPTQLinear, synthetic
+    from onecomp_runtime.layers import (Dsv4PackedLinear, PackedInt4Conv1d, PackedInt4ConvTranspose1d,
+                                        run_routed_experts)
+
+    res = {}
+    K = N = 5120
+    for wbits in (4, 8):
+        if wbits == 4:
+            nbytes = gptq_bytes(K, N, gs=128)
+            copies = math.ceil(2 * MALL_BYTES / nbytes)
+            _, mods = build_gptq(K, N, seed=20480, dev=dev, copies=copies, groupsize=128)
+        else:
+            G = K // 128
+            nbytes = K * N + G * N * 2 + G * (N // 4) * 4
+            copies = math.ceil(2 * MALL_BYTES / nbytes)
+            l8 = synthetic.gptq8_layer(K, N, seed=20481, groupsize=128)
+            mods = [PackedGPTQLinear(K, N, l8.qweight.to(dev), l8.scales.to(dev), l8.qzeros.to(dev), groupsize=128,
+                                     wbits=8) for _ in range(copies)]
+        for M in (1, 16):
+            x = synthetic.activations(M, K, seed=20482 + M).to(dev)
+            with torch.no_grad():
+                ms_eager = time_ms(lambda i: mods[i % copies](x), steps * 2, warmup)
+                ms = graph_ms([lambda m=m: m(x) for m in mods])
+            gbps = nbytes / (ms * 1e-3) / 1e9
+            res[f"gptq{wbits}_gs128_k5120_m{M}"] = {"us": ms * 1e3, "weight_GBps": gbps,
+                                                     "hbm_frac": gbps / HBM_PEAK_GBS, "us_eager": ms_eager * 1e3}
+        del mods
+        torch.cuda.empty_cache()
+    K, N = 7168, 2048
+    for wbits in (4, 2):
+        pk = synthetic.dsv4_layer(N, K, wbits=wbits, seed=20490 + wbits)
+        nbytes = N * K * wbits // 8 + 2 * (K // 128) * N * 2
+        copies = math.ceil(2 * MALL_BYTES / nbytes)
+        mods = [Dsv4PackedLinear(pk, buffer_device=dev) for _ in range(copies)]
+        x = synthetic.activations(1, K, seed=20492).to(dev)
+        with torch.no_grad():
+            ms = graph_ms([lambda m=m: m(x) for m in mods])
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        res[f"dsv4_int{wbits}_k7168_n2048_m1"] = {"us": ms * 1e3, "weight_GBps": gbps, "hbm_frac": gbps / HBM_PEAK_GBS}
+        del mods
+    # Host-resident int2 experts, 4 tokens x top-8 of 32: each call copies
+    # every routed expert (more than the stager's slots) and runs its GEMV.
+    E, T, topk = 32, 4, 8
+    packs = [synthetic.dsv4_layer(N, K, wbits=2, seed=20500 + e) for e in range(E)]
+    experts = [Dsv4PackedLinear(p, buffer_device="cpu") for p in packs]
+    ebytes = N * K // 4 + 2 * (K // 128) * N * 2
+    x = synthetic.activations(T, K, seed=20540).to(dev)
+    idss = [synthetic.router_topk(T, E, topk, seed=20541 + i).to(dev) for i in range(max(4, steps // 4))]
+    used = [len(set(ids.flatten().tolist())) for ids in idss]
+    with torch.no_grad():
+        ms = time_ms(lambda i: run_routed_experts(experts, x, idss[i % len(idss)]), len(idss), 2)
+    h2d = sum(used) / len(used) * ebytes
+    res["dsv4_int2_host_experts_t4_top8"] = {"ms": ms, "experts_per_call": sum(used) / len(used),
+                                             "h2d_GBps": h2d / (ms * 1e-3) / 1e9,
+                                             "pcie_frac": h2d / (ms * 1e-3) / 1e9 / PCIE_H2D_PEAK_GBS}
+    del experts, packs
+    # Packed convolutions (one batch, bf16).
+    cases = [("conv1d_512_512_k7_L8192", PackedInt4Conv1d, 512, 512, 7, dict(padding=3), 8192),
+             ("convT_1024_512_k16_s8_L1024", PackedInt4ConvTranspose1d, 1024, 512, 16, dict(stride=8), 1024)]
+    for name, cls, cin, cout, k, kw, L in cases:
+        rows, cols = (cout, cin * k) if cls is PackedInt4Conv1d else (cin, cout * k)
+        rl = synthetic.rtn_layer(rows, cols, seed=20550, groups=cols // 32)
+        mod = cls(cin, cout, k, qweight=rl.qweight_u8, scales=rl.scales, zeros=rl.zeros, cols=cols,
+                  pad_mode="none", **kw).to(dev)
+        x = synthetic.activations(cin, L, seed=20551).reshape(1, cin, L).to(dev)
+        with torch.no_grad():
+            y = mod(x)
+            ms = graph_ms([lambda: mod(x)] * 4)
+        flops = 2 * cin * cout * k * (y.shape[-1] if cls is PackedInt4Conv1d else L)
+        res[name] = {"us": ms * 1e3, "TFLOPs": flops / (ms * 1e-3) / 1e12,
+                     "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+    return res
+
+
 def cpu_model() -> str:
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -529,7 +613,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workloads", default="all",
-                    help="comma list of: m16,dit,padded,rtn,moe (the headline always runs)")
+                    help="comma list of: m16,dit,padded,rtn,moe,next (the headline always runs)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -545,7 +629,8 @@ def main() -> int:
         return 2
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    wl = {"m16", "dit", "padded", "rtn", "moe"} if args.workloads == "all" else set(args.workloads.split(","))
+    wl = ({"m16", "dit", "padded", "rtn", "moe", "next"} if args.workloads == "all"
+          else set(args.workloads.split(",")))
     if "none" in wl:
         wl = set()
 
@@ -583,6 +668,9 @@ def main() -> int:
     if "moe" in wl:
         log("moe")
         sub["moe_64x_top8"] = moe_workload(dev, max(5, args.steps // 2), 3)
+    if "next" in wl:
+        log("gs128 4/8-bit, DSV4, conv")
+        sub.update(next_rows_workload(dev, args.steps, args.warmup))
     torch.cuda.synchronize()
 
     cpu = None

@@ -1746,7 +1746,9 @@ int oc_dsv4_gemm(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_t
   if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(static_cast<char *>(workspace) + COUNTER_BYTES);
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf = x_dtype == OC_DTYPE_BF16;
-  if (wbits == 4) {
+  if (rows_gemv_applies(M, K, p.rtn_gs, wbits, scale_dtype, zero_dtype, row_bytes, qweight)) {
+    launch_rows_gemv(p, x_dtype, wbits == 4 ? FMT_DSV4_4 : FMT_DSV4_2, s);
+  } else if (wbits == 4) {
     if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_DSV4_4>(p, sp.tile, s);
     else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_DSV4_4>(p, sp.tile, s);
   } else {
@@ -1929,7 +1931,9 @@ int oc_rtn_linear(const void *x, int64_t ldx, int32_t x_dtype, int32_t M, int32_
   p.ksplit = 1;
   p.ksteps_per_split = K / 32;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (x_dtype == OC_DTYPE_BF16) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN>(p, pick, s);
+  if (rows_gemv_applies(M, K, K / G, 4, scale_dtype, zero_dtype, row_bytes, qweight_u8))
+    launch_rows_gemv(p, x_dtype, FMT_RTN, s);
+  else if (x_dtype == OC_DTYPE_BF16) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_RTN>(p, pick, s);
   else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_RTN>(p, pick, s);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;

@@ -208,6 +208,16 @@ int env_int(const char *name, int dflt);
 void plan_tiled(int M, int N, int K, int *wm, int *wn, int *kg, int *ksplit, int *ksteps_per_split);
 void launch_rtn_tiled(const GemmParams &p, int x_dtype, bool transposed, int wm, int wn, int kg, hipStream_t s);
 
+// Row-format GEMV for M <= 4 (oc_rows_gemv.hip): RTN nibble rows (fmt
+// FMT_RTN) and DSV4 int4 / int2 rows (FMT_DSV4_4 / FMT_DSV4_2), one wave per
+// output row, no workspace. rows_gemv_applies: M <= 4; K and the group size
+// multiples of one lane's 16 bytes of codes (32 columns at 4 bits, 64 at 2);
+// 16-byte aligned rows; 16-bit scales and zeros of one dtype; the activation
+// rows within 64 KB of LDS.
+bool rows_gemv_applies(int M, int K, int groupsize, int bits, int scale_dtype, int zero_dtype, int64_t row_bytes,
+                       const void *qweight);
+void launch_rows_gemv(const GemmParams &p, int x_dtype, int fmt, hipStream_t s);
+
 // Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
 // ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);

@@ -15,6 +15,16 @@ Workloads (K, N, M) follow the benchmark configurations:
     padded_gs26     M=256,  K=1040, N=3072, groupsize 26, v1
     rtn_moe         RTN linear M=512 K=1024 N=2048; RTN embedding 32768x1024, 4096 ids;
                     64-expert int4 gs32 K=4096 N=2048, 512 tokens top-8
+    next rows       GPTQ gs128 4-bit and 8-bit K=N=5120 at M=1/16; DSV4 int4/int2 gs128
+                    K=7168 N=2048 (device-resident at M=1; host-resident routed experts);
+                    packed Conv1d 512->512 k=7 and ConvTranspose1d 1024->512 k=16 stride 8
+
+8-bit GPTQ layers (``gptq8_layer``) draw codes 0..255, zeros 0..255 and scales
+``|N(0,1)| * 0.001 + 1e-4``; qweight packs 4 codes per int32 along K (code i at
+bits 8i), qzeros ``(Z - 1) & 0xFF`` (v1) 4 per int32 along N. DSV4 layers
+(``dsv4_layer``) draw codes ``[N, K]`` in 0..2^wbits-1 packed along K into
+uint8 (``8 // wbits`` per byte, code i at bits ``wbits * i``), integer zeros
+and scales ``[G, N]`` in fp16.
 """
 from __future__ import annotations
 
@@ -117,6 +127,53 @@ def rtn_layer(rows: int, K: int, *, seed: int, groups: int = 1) -> RTNLayer:
     zeros = torch.randint(0, 16, (rows, groups), generator=g).to(torch.float16)
     scales = (torch.randn(rows, groups, generator=g).abs() * 0.01 + 1e-3).to(torch.float16)
     return RTNLayer(rows, K, pack_nibbles(codes), scales, zeros, codes)
+
+
+def _pack_words(codes: torch.Tensor, bits: int, dim: int) -> torch.Tensor:
+    """int codes -> int32 words of 32 // bits codes along ``dim`` (code i at bits ``bits * i``)."""
+    per = 32 // bits
+    c = (codes.to(torch.int64) & ((1 << bits) - 1)).movedim(dim, 0)
+    n = c.shape[0]
+    c = c.reshape(n // per, per, *c.shape[1:])
+    word = torch.zeros((n // per, *c.shape[2:]), dtype=torch.int64)
+    for i in range(per):
+        word |= c[:, i] << (bits * i)
+    word = torch.where(word >= 2**31, word - 2**32, word)
+    return word.to(torch.int32).movedim(0, dim).contiguous()
+
+
+@dataclass
+class GPTQ8Layer:
+    K: int
+    N: int
+    groupsize: int
+    qweight: torch.Tensor  # int32 [K/4, N]
+    scales: torch.Tensor  # fp16 [G, N]
+    qzeros: torch.Tensor  # int32 [G, N/4] (v1: zero - 1)
+
+
+def gptq8_layer(K: int, N: int, *, seed: int, groupsize: int = 128) -> GPTQ8Layer:
+    g = torch.Generator().manual_seed(seed)
+    G = (K + groupsize - 1) // groupsize
+    codes = torch.randint(0, 256, (K, N), generator=g, dtype=torch.int32)
+    zeros = torch.randint(0, 256, (G, N), generator=g, dtype=torch.int32)
+    scales = (torch.randn(G, N, generator=g).abs() * 0.001 + 1e-4).to(torch.float16)
+    return GPTQ8Layer(K, N, groupsize, _pack_words(codes, 8, 0), scales, _pack_words((zeros - 1) & 0xFF, 8, 1))
+
+
+def dsv4_layer(N: int, K: int, *, wbits: int, seed: int, groupsize: int = 128) -> dict:
+    """A ``Dsv4PackedLinear`` pack: uint8 codes [N, K / (8 // wbits)], scales / zeros fp16 [G, N]."""
+    g = torch.Generator().manual_seed(seed)
+    per = 8 // wbits
+    G = (K + groupsize - 1) // groupsize
+    codes = torch.randint(0, 1 << wbits, (N, K), generator=g, dtype=torch.int32).reshape(N, K // per, per)
+    packed = torch.zeros((N, K // per), dtype=torch.int32)
+    for i in range(per):
+        packed |= codes[:, :, i] << (wbits * i)
+    scales = (torch.randn(G, N, generator=g).abs() * 0.02 + 1e-4).to(torch.float16)
+    zeros = torch.randint(0, 1 << wbits, (G, N), generator=g).to(torch.float16)
+    return {"qweight_packed": packed.to(torch.uint8), "scales": scales, "qzeros": zeros, "wbits": wbits,
+            "groupsize": groupsize, "in_features": K}
 
 
 @dataclass

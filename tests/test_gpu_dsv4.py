@@ -78,7 +78,7 @@ def test_dsv4_dequant_and_one_hot_gemm_bit_exact(wbits, case):
     mod = Dsv4PackedLinear(p, buffer_device=DEV)
     fused = mod._fused_ok(torch.zeros(1, dtype=dt))
     assert fused == (case != "ragged_k")
-    for M in (1, 40, 300):
+    for M in (1, 3, 40, 300):  # M <= 4: the row GEMV; larger: the tiled kernel
         ks = np.random.default_rng(M).integers(0, in_f, M)
         x = torch.zeros((M, in_f), dtype=dt)
         x[torch.arange(M), torch.from_numpy(ks)] = 1.0
@@ -93,7 +93,7 @@ def test_dsv4_gemm_matches_oracle_with_bias(wbits):
     p = _packed(2048, 7168, wbits, 128, seed=20450 + wbits)
     bias = torch.randn(2048, generator=torch.Generator().manual_seed(wbits))
     mod = Dsv4PackedLinear(p, bias=bias, buffer_device=DEV)
-    for M in (1, 8, 512):
+    for M in (1, 2, 4, 8, 512):
         x = torch.randn(M, 7168, generator=torch.Generator().manual_seed(M)).to(torch.bfloat16)
         say(f"dsv4 gemm wbits={wbits} M={M} K=7168 N=2048")
         ref = O.linear(np32(x), _ref_w(p, "bf16"), O.round_to(bias.numpy(), "bf16"), "bf16")

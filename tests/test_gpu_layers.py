@@ -26,10 +26,11 @@ def test_rtn_linear_workload():
     assert_gemm_close(mod(x.to(DEV)), ref, "rtn linear")
 
 
-@pytest.mark.parametrize("M", [1, 7, 64, 65, 200])
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 7, 64, 65, 200])
 @pytest.mark.parametrize("G", [1, 4])
 def test_rtn_linear_one_hot_bit_exact(M, G):
-    """The fused RTN kernel's per-op-rounded dequant is bit-exact."""
+    """The fused RTN kernels' per-op-rounded dequant is bit-exact (M <= 4: the
+    row GEMV, one wave per output row; larger M: the tiled kernel)."""
     from onecomp_runtime import PackedRTNLinear
 
     rng = np.random.default_rng(M + G)

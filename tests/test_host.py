@@ -126,6 +126,18 @@ def test_synthetic_packers_agree_with_oracle():
     assert padded.qweight.shape == (132, 8) and (padded.qweight[130:] == 0).all()
     rtn = synthetic.rtn_layer(4, 10, seed=3)
     assert np.array_equal(O.rtn_unpack(rtn.qweight_u8.numpy(), 10), rtn.codes.numpy())
+    # 8-bit GPTQ and DSV4 generators: the same draws packed by the oracle
+    l8 = synthetic.gptq8_layer(256, 64, seed=4, groupsize=128)
+    g = torch.Generator().manual_seed(4)
+    codes = torch.randint(0, 256, (256, 64), generator=g, dtype=torch.int32)
+    zeros = torch.randint(0, 256, (2, 64), generator=g, dtype=torch.int32)
+    assert np.array_equal(l8.qweight.numpy(), O.pack_rows(codes.numpy(), 8))
+    assert np.array_equal(l8.qzeros.numpy(), O.pack_zeros(zeros.numpy(), True, 8))
+    for wb in (2, 4):
+        pk = synthetic.dsv4_layer(64, 256, wbits=wb, seed=5)
+        g = torch.Generator().manual_seed(5)
+        c = torch.randint(0, 1 << wb, (64, 256), generator=g, dtype=torch.int32)
+        assert np.array_equal(pk["qweight_packed"].numpy(), O.dsv4_pack(c.numpy(), wb))
 
 
 def test_resolve_backend_and_dtype():
