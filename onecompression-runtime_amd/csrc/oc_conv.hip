@@ -42,6 +42,54 @@ __global__ __launch_bounds__(256) void im2col_kernel(const uint16_t *__restrict_
   a[idx] = (pos >= 0 && pos < L) ? x[(static_cast<int64_t>(b) * C + ci) * L + pos] : static_cast<uint16_t>(0);
 }
 
+// The same rows by tiles of I2C_TR output rows x I2C_CB input channels: the
+// tile's input window (channels ci0.., positions t0 * stride - pad_left ..,
+// W of them, zeros outside [0, L)) is read once into LDS with consecutive
+// positions per thread, then every output row's I2C_CB * k columns are
+// written as 16-byte chunks. A tile whose rows span two batch rows reads its
+// values from global memory instead.
+constexpr int I2C_TR = 64, I2C_CB = 32;
+inline int i2c_window(int k, int stride, int dilation) { return (I2C_TR - 1) * stride + (k - 1) * dilation + 1; }
+
+__global__ __launch_bounds__(256) void im2col_tile_kernel(const uint16_t *__restrict__ x, int C, int L, int k,
+                                                          int stride, int dilation, int pad_left, int T, int64_t r0,
+                                                          int rows, int K, int W, uint16_t *__restrict__ a) {
+  extern __shared__ uint16_t win[];  // [I2C_CB][W]
+  const int64_t ra = r0 + static_cast<int64_t>(blockIdx.x) * I2C_TR;  // first row of the tile
+  const int nrow = static_cast<int>(min<int64_t>(I2C_TR, r0 + rows - ra));
+  const int b0 = static_cast<int>(ra / T), t0 = static_cast<int>(ra % T);
+  const bool one_batch = (ra + nrow - 1) / T == b0;
+  const int ci0 = blockIdx.y * I2C_CB;
+  if (one_batch) {
+    const int p0 = t0 * stride - pad_left;
+    const uint16_t *xb = x + (static_cast<int64_t>(b0) * C + ci0) * L;
+    for (int i = threadIdx.x; i < I2C_CB * W; i += blockDim.x) {
+      const int c = i / W, pos = p0 + (i - c * W);
+      win[i] = pos >= 0 && pos < L ? xb[static_cast<int64_t>(c) * L + pos] : static_cast<uint16_t>(0);
+    }
+    __syncthreads();
+  }
+  const int CH = I2C_CB * k / 8;  // 16-byte chunks of one row in this channel block
+  for (int i = threadIdx.x; i < nrow * CH; i += blockDim.x) {
+    const int rr = i / CH, j = i - rr * CH;
+    const int64_t r = ra + rr;
+    uint32_t v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int cc = 8 * j + e, ci = cc / k, kk = cc - ci * k;
+      if (one_batch) {
+        v[e] = win[ci * W + rr * stride + kk * dilation];
+      } else {
+        const int64_t b = r / T;
+        const int pos = static_cast<int>(r % T) * stride + kk * dilation - pad_left;
+        v[e] = pos >= 0 && pos < L ? x[(b * C + ci0 + ci) * L + pos] : 0u;
+      }
+    }
+    *reinterpret_cast<uint4 *>(a + (r - r0) * K + static_cast<int64_t>(ci0) * k + 8 * j) =
+        make_uint4(v[0] | v[1] << 16, v[2] | v[3] << 16, v[4] | v[5] << 16, v[6] | v[7] << 16);
+  }
+}
+
 // out[b, o, t] for the chunk's rows: the K splits of the fp32 partials in
 // order, plus bias, rounded once. t fastest (coalesced stores).
 template <int DT>
@@ -243,9 +291,15 @@ int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32
     uint16_t *a = static_cast<uint16_t *>(workspace);
     float *part = reinterpret_cast<float *>(static_cast<char *>(workspace) +
                                             (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256);
-    hipLaunchKernelGGL(im2col_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * K)), dim3(256), 0, s,
-                       static_cast<const uint16_t *>(x), C_in, L, kernel_size, stride, dilation, pad_left, T_out, r0,
-                       rows, K, a);
+    const int W = i2c_window(kernel_size, stride, dilation);
+    if (C_in % I2C_CB == 0 && static_cast<size_t>(I2C_CB) * W * 2 <= 48 * 1024)
+      hipLaunchKernelGGL(im2col_tile_kernel, dim3((rows + I2C_TR - 1) / I2C_TR, C_in / I2C_CB), dim3(256),
+                         static_cast<size_t>(I2C_CB) * W * 2, s, static_cast<const uint16_t *>(x), C_in, L,
+                         kernel_size, stride, dilation, pad_left, T_out, r0, rows, K, W, a);
+    else
+      hipLaunchKernelGGL(im2col_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * K)), dim3(256), 0, s,
+                         static_cast<const uint16_t *>(x), C_in, L, kernel_size, stride, dilation, pad_left, T_out,
+                         r0, rows, K, a);
     const int ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype,
                                   K / G, G, 1, C_out, false, part, s);
     const dim3 grid(grid_1d(static_cast<int64_t>(rows) * C_out));
