@@ -1578,6 +1578,25 @@ Plan plan_tiled_only(int M, int N, int K_phys, bool has_kmap) {
   return sp;
 }
 
+// 8-bit GPTQ: batches of up to 16 rows on the balanced-range kernel's global
+// form (exact dequantization, MFMA; act-order rows gathered first) where it
+// applies (power-of-two group steps; ONECOMP_HIP_GEMV_STREAM=0, read per
+// call, keeps them on the tiled kernel), else the tiled kernel.
+Plan plan_int8(int M, int N, int K_phys, int group_rows, bool has_kmap) {
+  Plan sp = plan_tiled_only(M, N, K_phys, has_kmap);
+  if (M <= 16 && ilog2_exact(group_rows / 32) >= 0 && env_int("ONECOMP_HIP_GEMV_STREAM", 1) != 0) {
+    const int nwg = gemv_stream_global8_wgs(M, N, K_phys / 32, device_cus(), COUNTER_BYTES);
+    if (nwg > 0) {
+      sp.regime = OC_REGIME_SPLITK;
+      sp.stream_wgs = nwg;
+      sp.stream_global = true;
+      sp.ksplit = 1;
+      sp.ksteps_per_split = K_phys / 32;
+    }
+  }
+  return sp;
+}
+
 void plan_tiled(int M, int N, int K, int *wm, int *wn, int *kg, int *ksplit, int *ksteps_per_split) {
   const Plan sp = plan_tiled_only(M, N, K, false);
   *wm = sp.tile.wm;
@@ -1607,7 +1626,7 @@ extern "C" {
 
 size_t oc_int8_gemm_workspace_bytes(int32_t M, int32_t N, int32_t K_phys, int32_t group_rows, int32_t has_kmap) {
   if (M <= 0 || N <= 0 || K_phys <= 0 || group_rows <= 0) return 0;
-  return workspace_bytes(plan_tiled_only(M, N, K_phys, has_kmap != 0), M, N, K_phys);
+  return workspace_bytes(plan_int8(M, N, K_phys, group_rows, has_kmap != 0), M, N, K_phys);
 }
 
 int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t K_logical, const int32_t *qt,
@@ -1637,7 +1656,10 @@ int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   const int64_t tiles = (N + TILE_N - 1) / TILE_N;
   if (tiles * (K_phys / 32) * 512 >= (1LL << 31))
     return fail(OC_ERR_UNSUPPORTED, "layer too large: packed words of 2 GiB or more");
-  const Plan sp = plan_tiled_only(M, N, K_phys, kmap != nullptr);
+  Plan sp = plan_int8(M, N, K_phys, group_rows, kmap != nullptr);
+  // The global form addresses activation rows with 32-bit offsets.
+  if (sp.stream_wgs > 0 && (static_cast<int64_t>(M) - 1) * (kmap ? K_phys : lda) * 2 + K_phys * 2 >= (int64_t{1} << 31))
+    sp = plan_tiled_only(M, N, K_phys, kmap != nullptr);
   const size_t need = workspace_bytes(sp, M, N, K_phys);
   if (need > 0) {
     if (!workspace || workspace_bytes_given < need)
@@ -1674,7 +1696,11 @@ int oc_int8_gemm(const void *a, int64_t lda, int32_t a_dtype, int32_t M, int32_t
   }
   if (sp.ksplit > 1) p.partials = reinterpret_cast<float *>(ws_after_counters + gather_bytes(sp, M, K_phys));
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf && sbf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
+  if (sp.stream_wgs > 0) {
+    p.a_bytes = (static_cast<int64_t>(M) - 1) * p.lda * 2 + static_cast<int64_t>(sp.gather ? K_phys : K_logical) * 2;
+    p.counters = static_cast<int *>(workspace);
+    launch_gptq8_gemv_stream(p, a_dtype, scale_dtype, sp.stream_wgs, s);
+  } else if (bf && sbf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
   else if (bf) launch_tiled<OC_DTYPE_BF16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);
   else if (sbf) launch_tiled<OC_DTYPE_F16, OC_DTYPE_BF16, FMT_GPTQ8>(p, sp.tile, s);
   else launch_tiled<OC_DTYPE_F16, OC_DTYPE_F16, FMT_GPTQ8>(p, sp.tile, s);

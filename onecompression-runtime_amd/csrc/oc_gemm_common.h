@@ -245,6 +245,10 @@ int gemv_stream_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
 // The same ranges for 3..16 rows read from global memory in physical row order
 // (no staging; for rows beyond LDS when whole tiles would load CUs unevenly).
 int gemv_stream_global_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
+// 8-bit tile16x8 layers at M <= 16: launch width of the global form (0: not
+// applicable) and its launch (activation rows in physical order).
+int gemv_stream_global8_wgs(int M, int N, int KS, int cus, size_t cell_bytes);
+void launch_gptq8_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s);
 void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, bool global_rows,
                              hipStream_t s);
 

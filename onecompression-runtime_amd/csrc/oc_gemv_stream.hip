@@ -84,8 +84,10 @@ int stream_slots(int64_t tiles, int QT, int nwg) {
 }  // namespace
 
 // AL: K steps per tile a multiple of 4, so unit u starts at byte 1024 u of
-// the tile16 words and at group (4 u) >> gshift of the scales and zeros.
-template <int DT, int SDT, int MR, int SX, int PF, bool AL>
+// the tile16 words (2048 u for 8-bit) and at group (4 u) >> gshift of the
+// scales and zeros. WB: code bits, 4 (tile16) or 8 (tile16x8: global form
+// only; a column's K step is 8 words, 32 bytes, 4 zero bytes per word).
+template <int DT, int SDT, int MR, int SX, int PF, bool AL, int WB = 4>
 __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   constexpr uint32_t MAGIC = DT == OC_DTYPE_BF16 ? 0x43004300u : 0x64006400u;
   constexpr bool MF = MR > 2;     // MFMA inner product (rows 4 g + i of lane (g, c))
@@ -93,6 +95,9 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   constexpr int SB = MF ? 1 : 3;  // staged octets per thread per batch
   static_assert(!MF || MR == 4 || MR == 8 || MR == 16, "MFMA rows");
   static_assert(!GL || MF, "global activation rows take the MFMA form");
+  static_assert(WB == 4 || (WB == 8 && GL), "8-bit codes take the global form");
+  constexpr uint32_t STEPB = WB == 8 ? 512u : 256u;  // bytes of one tile and K step
+  constexpr uint32_t ZSTR = WB == 8 ? 16u : 8u;      // zero bytes of one tile and group
   extern __shared__ __attribute__((aligned(16))) uint4 sx_lds[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -266,10 +271,12 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     uint32_t s[4];
     uint32_t z;
   };
-  // Global form: the dot2 form's weight loads plus the A operand of lane
-  // (h, r): row r's 32 activations of K step 4 q + h (four 16-byte loads).
+  // Global form: the dot2 form's weight loads (8-bit: two 16-byte loads, the
+  // column's 8 words of the step) plus the A operand of lane (h, r): row r's
+  // 32 activations of K step 4 q + h (four 16-byte loads).
   struct StageGl {
     uint4 q;
+    uint4 q2;
     uint32_t s;
     uint32_t z;
     uint32_t x[16];
@@ -281,28 +288,30 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
   // past the wave's range get an offset beyond every buffer (zero, no
   // memory access).
   const int G = p.G, gshift = p.gshift, gs2 = min(gshift, 2);
-  const __amdgpu_buffer_rsrc_t q_rs = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
+  const __amdgpu_buffer_rsrc_t q_rs = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * STEPB);
   const __amdgpu_buffer_rsrc_t s_rs = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * G * 32);
-  const __amdgpu_buffer_rsrc_t z_rs = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * G * 8);
+  const __amdgpu_buffer_rsrc_t z_rs = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * G * ZSTR);
   constexpr bool MFL = MF && !GL;  // per-octet weight loads (staged MFMA form)
-  const uint32_t q_lane = MFL ? static_cast<uint32_t>(c * 16 + 4 * h) : lane * 16u;  // + 256 j (MFMA form)
+  const uint32_t q_lane = MFL ? static_cast<uint32_t>(c * 16 + 4 * h)
+                              : WB == 8 ? static_cast<uint32_t>(512 * h + 32 * c) : lane * 16u;  // + 256 j (MFMA form)
   const uint32_t s_lane = MFL ? static_cast<uint32_t>(c) * 2u                          // + 32 (j >> gs2)
                               : static_cast<uint32_t>((h >> gs2) * 16 + c) * 2u;      // group of K step 4 q + h
   // Global form: row c of the activations (rows past M read nowhere).
   const __amdgpu_buffer_rsrc_t a_rs = buffer_rsrc(p.a, GL ? p.a_bytes : 0);
   const uint32_t a_row = GL && c < M ? static_cast<uint32_t>(c * p.lda * 2) : 0xFFFFF000u;
-  const uint32_t z_lane = static_cast<uint32_t>((h >> gs2) * 2 + (c >> 3)) * 4u;
+  const uint32_t z_lane = WB == 8 ? static_cast<uint32_t>((h >> gs2) * 4 + (c >> 2)) * 4u
+                                  : static_cast<uint32_t>((h >> gs2) * 2 + (c >> 3)) * 4u;
   constexpr uint32_t NOWHERE = 0xFFFFF000u;
   const int w_u0 = u0 + wave;  // this wave's first unit; it takes every SW-th from there
   int pu = w_u0;               // producer: next unit to load
   auto load = [&](Stage &S) {
     uint32_t qb, gb;
     if constexpr (AL) {
-      qb = static_cast<uint32_t>(pu) * 1024u;
+      qb = static_cast<uint32_t>(pu) * (4 * STEPB);
       gb = static_cast<uint32_t>(4 * pu) >> gshift;
     } else {
       const int tt = pu / QT, qq = pu - tt * QT;
-      qb = static_cast<uint32_t>(tt * KS + 4 * qq) * 256u;
+      qb = static_cast<uint32_t>(tt * KS + 4 * qq) * STEPB;
       gb = static_cast<uint32_t>(tt * G + ((4 * qq) >> gshift));
     }
     const bool in = pu < u1;
@@ -310,6 +319,12 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
     if constexpr (GL) {
       const auto q = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 0,CPOL_WEIGHT_STREAM);
       S.q = make_uint4(q[0], q[1], q[2], q[3]);
+      if constexpr (WB == 8) {
+        const auto q2 = __builtin_amdgcn_raw_buffer_load_b128(q_rs, qo, 16, CPOL_WEIGHT_STREAM);
+        S.q2 = make_uint4(q2[0], q2[1], q2[2], q2[3]);
+      } else {
+        S.q2 = make_uint4(0, 0, 0, 0);
+      }
       S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0,CPOL_WEIGHT_STREAM);
       const int ks = 4 * (pu % QT) + h;  // this lane's K step (steps past KS read zeros)
       const bool a_in = in && ks < KS && a_row != NOWHERE;
@@ -330,7 +345,7 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
       S.q = make_uint4(q[0], q[1], q[2], q[3]);
       S.s = __builtin_amdgcn_raw_buffer_load_b16(s_rs, so, 0,CPOL_WEIGHT_STREAM);
     }
-    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * 8u : NOWHERE), 0,CPOL_WEIGHT_STREAM);
+    S.z = __builtin_amdgcn_raw_buffer_load_b32(z_rs, z_lane + (in ? gb * ZSTR : NOWHERE), 0,CPOL_WEIGHT_STREAM);
     pu += SW;
   };
   // Activations are staged before the weight prefetch goes out: memory
@@ -416,12 +431,15 @@ __global__ __launch_bounds__(SNT) void gemv_stream_kernel(GemmParams p) {
         // Exact dequantization (the scale inside B), so the unit's MFMAs
         // accumulate across its four K steps: MFMA j takes word j of every
         // lane (octet j of K step 4 qq + h) against row r's matching octet.
-        const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c));
-        const uint32_t qw[4] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w};
+        const uint32_t qw[8] = {cur.q.x, cur.q.y, cur.q.z, cur.q.w, cur.q2.x, cur.q2.y, cur.q2.z, cur.q2.w};
         v4f32 av = {acc[0], acc[1], acc[2], acc[3]};
+        const float s8 = scale_f32<SDT>(cur.s);
+        const float zs8 = -s8 * static_cast<float>((cur.z >> (8 * (c & 3))) & 0xFFu);
+        const GroupParam gp = make_group_param(scale_f32<SDT>(cur.s), tile_zero(cur.z, c));
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const uint4 b = dequant8<DT>(qw[j], gp);
+          // 8-bit: words 2j, 2j + 1 hold the K rows 8j .. 8j + 7 (4 codes each)
+          const uint4 b = WB == 8 ? dequant8_u8<DT>(qw[2 * j], qw[2 * j + 1], s8, zs8) : dequant8<DT>(qw[j], gp);
           const uint4 xa = make_uint4(cur.x[4 * j], cur.x[4 * j + 1], cur.x[4 * j + 2], cur.x[4 * j + 3]);
           av = mfma16x16x32<DT>(xa, b, av);
         }
@@ -587,9 +605,9 @@ int gemv_stream_global_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
   return static_cast<int>(nwg);
 }
 
-template <int DT, int SDT, int MR, int SX, int PF, bool AL>
+template <int DT, int SDT, int MR, int SX, int PF, bool AL, int WB = 4>
 static void launch_stream_t(const GemmParams &p, int nwg, hipStream_t s) {
-  auto kern = gemv_stream_kernel<DT, SDT, MR, SX, PF, AL>;
+  auto kern = gemv_stream_kernel<DT, SDT, MR, SX, PF, AL, WB>;
   static std::atomic<uint64_t> attr_set{0};
   int dev = 0;
   (void)hipGetDevice(&dev);
@@ -631,6 +649,48 @@ static void launch_stream_m(const GemmParams &p, int nwg, bool g, hipStream_t s)
     case 8: launch_stream_x<DT, SDT, 8>(p, nwg, g, s); break;
     default: launch_stream_x<DT, SDT, 16>(p, nwg, g, s); break;
   }
+}
+
+// 8-bit layers (tile16x8) at M <= 16: the global form on the same ranges,
+// rows staged as 4, 8 or 16 (M <= 2 multiply rows past M that read nowhere).
+int gemv_stream_global8_wgs(int M, int N, int KS, int cus, size_t cell_bytes) {
+  if (M < 1 || M > 16) return 0;
+  const int MR = std::max(4, stream_rows(M));
+  const int64_t tiles = (N + TILE_N - 1) / TILE_N, QT = (KS + 3) / 4;
+  int64_t nwg = cus;
+  if (tiles < cus) {
+    // Narrow layers: two workgroups per tile, each exactly half of it.
+    if (2 * tiles > cus || QT % 2 != 0) return 0;
+    nwg = 2 * tiles;
+  }
+  const int64_t q1 = tiles * QT / nwg + 1;
+  if ((q1 + QT - 1) / QT + 1 > SNTL) return 0;
+  const int nslots = stream_slots(tiles, static_cast<int>(QT), static_cast<int>(nwg));
+  if (gemv_stream_lds_bytes(MR, KS, nslots, true) > 160 * 1024 - 64) return 0;
+  if (static_cast<size_t>(nwg) * MR * 16 * sizeof(unsigned long long) > cell_bytes) return 0;
+  return static_cast<int>(nwg);
+}
+
+template <int DT, int SDT, int MR>
+static void launch_stream8_al(const GemmParams &p, int nwg, hipStream_t s) {
+  if (p.KS % 4 == 0) launch_stream_t<DT, SDT, MR, SX_GLOBAL, 2, true, 8>(p, nwg, s);
+  else launch_stream_t<DT, SDT, MR, SX_GLOBAL, 2, false, 8>(p, nwg, s);
+}
+
+template <int DT, int SDT>
+static void launch_stream8_m(const GemmParams &p, int nwg, hipStream_t s) {
+  const int MR = std::max(4, stream_rows(p.M));
+  if (MR == 4) launch_stream8_al<DT, SDT, 4>(p, nwg, s);
+  else if (MR == 8) launch_stream8_al<DT, SDT, 8>(p, nwg, s);
+  else launch_stream8_al<DT, SDT, 16>(p, nwg, s);
+}
+
+void launch_gptq8_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, hipStream_t s) {
+  const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
+  if (bf && sbf) launch_stream8_m<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, nwg, s);
+  else if (bf) launch_stream8_m<OC_DTYPE_BF16, OC_DTYPE_F16>(p, nwg, s);
+  else if (sbf) launch_stream8_m<OC_DTYPE_F16, OC_DTYPE_BF16>(p, nwg, s);
+  else launch_stream8_m<OC_DTYPE_F16, OC_DTYPE_F16>(p, nwg, s);
 }
 
 void launch_gptq_gemv_stream(const GemmParams &p, int a_dtype, int scale_dtype, int nwg, bool global_rows,
