@@ -292,7 +292,8 @@ class _HipGPTQLinear(torch.nn.Module):
         if _profile.PROFILE_SHAPES:
             _profile.record(self._kind, a_2d.shape[0], self.in_features, self.out_features)
         call, buf = self._call, self._buffers
-        if call is None or call.qt is not buf.get("qweight_tiled") or call.w.st is not buf.get("scales_tiled"):
+        if (call is None or call.qt is not buf.get("qweight_tiled") or call.w.st is not buf.get("scales_tiled")
+                or call.mid[1] != call.qt.data_ptr()):
             w = self.tiled()
             call = self._call = kernels.LayerCall(w, self.in_features, self.kmap, self.kinv)
         c = call(a_2d, bias)

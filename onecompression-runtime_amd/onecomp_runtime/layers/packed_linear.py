@@ -11,7 +11,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .. import kernels
+from .. import _hip, kernels
 
 
 class PackedRTNLinear(nn.Module):
@@ -93,11 +93,32 @@ class PackedEmbedding(nn.Module):
         self.register_buffer("zeros", zeros.contiguous())
         self.register_buffer("bad_id_flag", torch.zeros(1, dtype=torch.int32,
                                                         device=qweight_u8.device), persistent=False)
+        self._call = None  # the table's fixed call arguments, bound at the first device forward
+
+    def _bind(self, q, sc, z, flag) -> tuple:
+        dtype = sc.dtype if sc.dtype.is_floating_point else torch.float16
+        mid = (q.data_ptr(), q.shape[0], q.shape[1], sc.data_ptr(), _hip.dtype_code(sc.dtype), z.data_ptr(),
+               _hip.dtype_code(z.dtype), sc.shape[1], self.embedding_dim)
+        return (q, sc, z, flag, q.get_device(), dtype, mid, _hip.dtype_code(dtype), flag.data_ptr())
 
     def forward(self, input_ids: torch.Tensor) -> torch.Tensor:
-        dtype = self.scales.dtype if self.scales.dtype.is_floating_point else torch.float16
-        rows = kernels.rtn_embedding(input_ids, self.qweight_u8, self.scales, self.zeros,
-                                     self.embedding_dim, dtype, self.bad_id_flag)
+        b = self._buffers
+        q, sc, z, flag = b["qweight_u8"], b["scales"], b["zeros"], b["bad_id_flag"]
+        call = self._call
+        if q.is_cuda and (call is None or call[0] is not q or call[1] is not sc or call[2] is not z
+                          or call[3] is not flag or call[6][0] != q.data_ptr()):
+            call = self._call = self._bind(q, sc, z, flag)
+        ids = input_ids
+        if (call is not None and q.is_cuda and ids.is_cuda and ids.dtype is torch.int64 and ids.is_contiguous()
+                and ids.get_device() == call[4] and sc.is_cuda and z.is_cuda and flag.is_cuda):
+            # Fast path: ids already int64 and contiguous on the table's device.
+            T = ids.numel()
+            rows = torch.empty((T, self.embedding_dim), dtype=call[5], device=ids.device)
+            _hip.check(_hip.lib().oc_rtn_embedding(ids.data_ptr(), T, *call[6], rows.data_ptr(), call[7], call[8],
+                                                   _hip._raw_stream(call[4])), "oc_rtn_embedding")
+        else:
+            dtype = sc.dtype if sc.dtype.is_floating_point else torch.float16
+            rows = kernels.rtn_embedding(input_ids, q, sc, z, self.embedding_dim, dtype, flag)
         return rows.reshape(*input_ids.shape, self.embedding_dim)
 
     def check_ids(self) -> None:
