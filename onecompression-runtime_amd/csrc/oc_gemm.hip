@@ -488,11 +488,15 @@ __global__ __launch_bounds__(256 * KG) void gemm_tiled_kernel(GemmParams p) {
   auto &As = As_all[grp];
   const int wave = tid >> 6, lane = tid & 63;
   const int quad = lane >> 4, c16 = lane & 15;
-  const int n0 = blockIdx.x * BN;
+  // The column blocks of one row block on one XCD (they share its activation
+  // rows in that XCD's L2).
+  const int blk = xcd_block(blockIdx.y * gridDim.x + blockIdx.x, gridDim.x * gridDim.y);
+  const int bxx = blk % gridDim.x, byy = blk / gridDim.x;
+  const int n0 = bxx * BN;
   const int tw = n0 / TILE_N + wave * WN;  // first tile of this wave
   const int last_tile = (p.N - 1) / TILE_N;
   const uint16_t *a = static_cast<const uint16_t *>(p.a);
-  const int m0 = blockIdx.y * BM;
+  const int m0 = byy * BM;
   const int wg_begin = blockIdx.z * p.ksteps_per_split;
   const int wg_end = min(wg_begin + p.ksteps_per_split, p.KS);
   const int part = (max(wg_end - wg_begin, 0) + KG - 1) / KG;  // steps per K group (the last may have fewer)

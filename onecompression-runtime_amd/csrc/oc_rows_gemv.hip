@@ -40,7 +40,9 @@ __global__ __launch_bounds__(64 * RG_WAVES) void rows_gemv_kernel(GemmParams p) 
   extern __shared__ __attribute__((aligned(16))) uint4 xs[];  // [MR][NOP] activation octets, permuted
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int n = blockIdx.x * RG_WAVES + wave;
+  // Workgroups of neighbouring rows on one XCD: they share the lines of the
+  // [groups][N] scales and zeros.
+  const int n = xcd_block(blockIdx.x, gridDim.x) * RG_WAVES + wave;
   const int nr = min(n, p.N - 1);  // rows past N load a valid row; nothing is stored for them
   const int K = p.K_logical, NO = K >> 3;
   const int NL = (NO + OB - 1) / OB;  // wave loads per row
