@@ -91,22 +91,55 @@ __global__ __launch_bounds__(256) void im2col_tile_kernel(const uint16_t *__rest
 }
 
 // out[b, o, t] for the chunk's rows: the K splits of the fp32 partials in
-// order, plus bias, rounded once. t fastest (coalesced stores).
+// order, plus bias, rounded once. Tiles of EP_R rows x EP_N columns pass
+// through LDS: the partials are read along their rows (columns fastest) and
+// the outputs written along t, both coalesced.
+constexpr int EP_R = 64, EP_N = 64;
 template <int DT>
-__global__ __launch_bounds__(256) void conv1d_epilogue_kernel(const float *__restrict__ part, int ksplit, int rows,
-                                                              int N, int T, int64_t r0, const void *bias,
-                                                              int bias_dtype, void *__restrict__ y) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= static_cast<int64_t>(rows) * N) return;
-  const int r = static_cast<int>(idx % rows);
-  const int n = static_cast<int>(idx / rows);
+__global__ __launch_bounds__(256) void conv1d_epilogue_tile_kernel(const float *__restrict__ part, int ksplit,
+                                                                   int rows, int N, int T, int64_t r0,
+                                                                   const void *bias, int bias_dtype,
+                                                                   void *__restrict__ y) {
+  __shared__ float tile[EP_R][EP_N + 1];
+  const int rb = static_cast<int>(blockIdx.x) * EP_R, nb = static_cast<int>(blockIdx.y) * EP_N;
   const int64_t mn = static_cast<int64_t>(rows) * N;
-  float v = 0.f;
-  for (int s = 0; s < ksplit; ++s) v += part[s * mn + static_cast<int64_t>(r) * N + n];
-  if (bias) v += load_any_f32(bias, n, bias_dtype);
-  const int64_t rr = r0 + r;
-  const int64_t b = rr / T, t = rr % T;
-  store_c<DT>(y, (b * N + n) * T + t, v);
+  constexpr int U = EP_R * EP_N / 256;
+  int64_t e[U];
+  float v[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u, rr = i / EP_N, nn = i % EP_N;
+    e[u] = rb + rr < rows && nb + nn < N ? static_cast<int64_t>(rb + rr) * N + nb + nn : -1;
+    v[u] = 0.f;
+  }
+  for (int sp = 0; sp < ksplit; ++sp) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (e[u] >= 0) v[u] += part[sp * mn + e[u]];
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    tile[i / EP_N][i % EP_N] = v[u];
+  }
+  __syncthreads();
+  const int64_t ra = r0 + rb;
+  const int64_t b0 = ra / T;
+  const int t0 = static_cast<int>(ra - b0 * T);
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int i = threadIdx.x + 256 * u, nn = i / EP_R, rr = i % EP_R, n = nb + nn;
+    if (rb + rr >= rows || n >= N) continue;
+    float val = tile[rr][nn];
+    if (bias) val += load_any_f32(bias, n, bias_dtype);
+    int t = t0 + rr;
+    int64_t b = b0;
+    while (t >= T) {  // rows of the tile past the end of a batch row
+      t -= T;
+      ++b;
+    }
+    store_c<DT>(y, (b * N + n) * T + t, val);
+  }
 }
 
 // Transposed-weight re-layout: codes [C_in rows, cols] (RTN nibbles) ->
@@ -169,6 +202,80 @@ __global__ __launch_bounds__(256) void col2im_add_kernel(const float *__restrict
   acc[static_cast<int64_t>(o) * Lout + t] += v;
 }
 
+// The same sums by tiles of CT_T output positions x CT_O output channels: the
+// input rows that reach the tile (JR of them, the K splits already added) are
+// read into LDS along the GEMM's columns, then each output adds its taps (kk
+// ascending, as above). FINAL (one chunk covers the whole input): the output
+// is written directly with the bias, rounded once (no accumulator pass).
+constexpr int CT_T = 64, CT_O = 16;
+__host__ __device__ inline int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+inline int col2im_rows(int k, int stride, int dilation) { return (CT_T - 1 + (k - 1) * dilation) / stride + 2; }
+
+template <int DT, bool FINAL>
+__global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restrict__ part, int ksplit, int rows, int O,
+                                                          int k, int stride, int dilation, int padding, int j0,
+                                                          int t_lo, int t_hi, int Lout, int JR,
+                                                          float *__restrict__ acc, const void *bias, int bias_dtype,
+                                                          void *__restrict__ y) {
+  extern __shared__ float zs[];  // [JR][CT_O * k]
+  const int t0 = t_lo + static_cast<int>(blockIdx.x) * CT_T, o0 = static_cast<int>(blockIdx.y) * CT_O;
+  const int N = O * k, W = CT_O * k;
+  const int wlim = min(W, (O - o0) * k);  // columns of the tile's channels that exist
+  const int64_t mn = static_cast<int64_t>(rows) * N;
+  const int jlo = floor_div(t0 + padding - (k - 1) * dilation, stride);  // first input position reaching the tile
+  const int total = JR * W;
+  // U independent loads per thread in flight (one chain per element).
+  constexpr int U = 4;
+  for (int i0 = threadIdx.x; i0 < total; i0 += U * 256) {
+    int64_t e[U];
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = i0 + u * 256;
+      const int jj = i / W, c = i - jj * W;
+      const int j = jlo + jj - j0;  // row of the chunk
+      e[u] = i < total && j >= 0 && j < rows && c < wlim ? static_cast<int64_t>(j) * N + static_cast<int64_t>(o0) * k + c
+                                                          : -1;
+      v[u] = 0.f;
+    }
+    for (int sp = 0; sp < ksplit; ++sp) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (e[u] >= 0) v[u] += part[sp * mn + e[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (i0 + u * 256 < total) zs[i0 + u * 256] = v[u];
+  }
+  __syncthreads();
+  const int dmax = (k - 1) * dilation;
+  for (int i = threadIdx.x; i < CT_T * CT_O; i += 256) {
+    const int ol = i / CT_T, t = t0 + (i - ol * CT_T), o = o0 + ol;
+    if (t >= t_hi || o >= O) continue;
+    // Taps kk ascending = input positions j descending (j * stride = t + padding - kk * dilation); only the
+    // positions that are whole multiples are visited.
+    const int base = t + padding;
+    float v = 0.f;
+    for (int j = floor_div(base, stride); j >= jlo; --j) {
+      const int d = base - j * stride;  // kk * dilation
+      if (d > dmax || j < j0) break;
+      if (j >= j0 + rows) continue;
+      int kk = d;
+      if (dilation != 1) {
+        if (d % dilation != 0) continue;
+        kk = d / dilation;
+      }
+      v += zs[(j - jlo) * W + ol * k + kk];
+    }
+    if constexpr (FINAL) {
+      if (bias) v += load_any_f32(bias, o, bias_dtype);
+      store_c<DT>(y, static_cast<int64_t>(o) * Lout + t, v);
+    } else {
+      acc[static_cast<int64_t>(o) * Lout + t] += v;
+    }
+  }
+}
+
 template <int DT>
 __global__ __launch_bounds__(256) void finish_kernel(const float *__restrict__ acc, int O, int Lout, const void *bias,
                                                      int bias_dtype, void *__restrict__ y) {
@@ -185,13 +292,18 @@ __global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, in
   if (idx < n) p[idx] = 0.f;
 }
 
-// Rows per chunk: a bounded workspace (activation rows plus fp32 partials).
-constexpr size_t CONV_CHUNK_BYTES = size_t{64} << 20;
+// Rows per chunk: a bounded workspace (activation rows plus fp32 partials),
+// the rows spread evenly over the chunks (multiples of 256), so that no
+// chunk is a small remainder whose GEMM fills a fraction of the chip.
+constexpr size_t CONV_CHUNK_BYTES = size_t{128} << 20;
 
 int chunk_rows(int64_t total, int K, int N) {
   const int64_t per_row = 2 * static_cast<int64_t>(K) + 4 * static_cast<int64_t>(N);
-  int64_t r = std::max<int64_t>(256, static_cast<int64_t>(CONV_CHUNK_BYTES) / per_row) / 256 * 256;
-  return static_cast<int>(std::min<int64_t>(total, r));
+  const int64_t rmax = std::max<int64_t>(256, static_cast<int64_t>(CONV_CHUNK_BYTES) / per_row) / 256 * 256;
+  if (total <= rmax) return static_cast<int>(total);
+  const int64_t chunks = (total + rmax - 1) / rmax;
+  const int64_t r = ((total + chunks - 1) / chunks + 255) / 256 * 256;
+  return static_cast<int>(std::min(r, rmax));
 }
 
 // Workspace of one chunk of `rows` rows: activations, then fp32 partials.
@@ -302,12 +414,12 @@ int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32
                          r0, rows, K, a);
     const int ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype,
                                   K / G, G, 1, C_out, false, part, s);
-    const dim3 grid(grid_1d(static_cast<int64_t>(rows) * C_out));
+    const dim3 grid((rows + EP_R - 1) / EP_R, (C_out + EP_N - 1) / EP_N);
     if (x_dtype == OC_DTYPE_BF16)
-      hipLaunchKernelGGL(conv1d_epilogue_kernel<OC_DTYPE_BF16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
+      hipLaunchKernelGGL(conv1d_epilogue_tile_kernel<OC_DTYPE_BF16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
                          T_out, r0, bias, bias_dtype, y);
     else
-      hipLaunchKernelGGL(conv1d_epilogue_kernel<OC_DTYPE_F16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
+      hipLaunchKernelGGL(conv1d_epilogue_tile_kernel<OC_DTYPE_F16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,
                          T_out, r0, bias, bias_dtype, y);
   }
   OC_RETURN_LAUNCH_STATUS();
@@ -371,8 +483,14 @@ int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C
   const int R = chunk_rows(L_in, C_in, N);
   const int64_t outs = static_cast<int64_t>(C_out) * L_out;
   const int span_max = (R - 1) * stride + (kernel_size - 1) * dilation + 1;
+  const int JR = col2im_rows(kernel_size, stride, dilation);
+  const size_t tile_lds = static_cast<size_t>(JR) * CT_O * kernel_size * 4;
+  const bool tiled = tile_lds <= 48 * 1024;
+  const bool direct = tiled && R >= L_in;  // one chunk: outputs written by the col2im pass itself
+  const bool bf = x_dtype == OC_DTYPE_BF16;
   for (int b = 0; b < B; ++b) {
-    hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_1d(outs)), dim3(256), 0, s, acc, outs);
+    void *yb = static_cast<char *>(y) + static_cast<size_t>(b) * outs * 2;
+    if (!direct) hipLaunchKernelGGL(zero_f32_kernel, dim3(grid_1d(outs)), dim3(256), 0, s, acc, outs);
     for (int j0 = 0; j0 < L_in; j0 += R) {
       const int rows = std::min(R, L_in - j0);
       uint16_t *a = reinterpret_cast<uint16_t *>(chunk_ws);
@@ -381,15 +499,35 @@ int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C
                          static_cast<const uint16_t *>(x), C_in, L_in, b, j0, rows, a);
       const int ksplit = chunk_gemm(a, x_dtype, rows, C_in, qweight_t, C_in / 2, scales_t, scale_dtype, zeros_t,
                                     scale_dtype, N / G, 0, 0, N, true, part, s);
-      const int t_lo = std::max(0, j0 * stride - padding);
-      const int t_hi = std::min(L_out, (j0 + rows - 1) * stride + (kernel_size - 1) * dilation - padding + 1);
+      int t_lo = std::max(0, j0 * stride - padding);
+      int t_hi = std::min(L_out, (j0 + rows - 1) * stride + (kernel_size - 1) * dilation - padding + 1);
+      if (direct) {
+        t_lo = 0;  // every output, tapped or not (bias only)
+        t_hi = L_out;
+      }
       if (t_hi <= t_lo) continue;
       (void)span_max;
-      hipLaunchKernelGGL(col2im_add_kernel, dim3(grid_1d(static_cast<int64_t>(t_hi - t_lo) * C_out)), dim3(256), 0,
-                         s, part, ksplit, rows, C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi, L_out,
-                         acc);
+      if (tiled) {
+        const dim3 g((t_hi - t_lo + CT_T - 1) / CT_T, (C_out + CT_O - 1) / CT_O);
+        if (direct && bf)
+          hipLaunchKernelGGL((col2im_tile_kernel<OC_DTYPE_BF16, true>), g, dim3(256), tile_lds, s, part, ksplit, rows,
+                             C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi, L_out, JR, acc, bias,
+                             bias_dtype, yb);
+        else if (direct)
+          hipLaunchKernelGGL((col2im_tile_kernel<OC_DTYPE_F16, true>), g, dim3(256), tile_lds, s, part, ksplit, rows,
+                             C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi, L_out, JR, acc, bias,
+                             bias_dtype, yb);
+        else
+          hipLaunchKernelGGL((col2im_tile_kernel<OC_DTYPE_F16, false>), g, dim3(256), tile_lds, s, part, ksplit, rows,
+                             C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi, L_out, JR, acc, bias,
+                             bias_dtype, yb);
+      } else {
+        hipLaunchKernelGGL(col2im_add_kernel, dim3(grid_1d(static_cast<int64_t>(t_hi - t_lo) * C_out)), dim3(256),
+                           0, s, part, ksplit, rows, C_out, kernel_size, stride, dilation, padding, j0, t_lo, t_hi,
+                           L_out, acc);
+      }
     }
-    void *yb = static_cast<char *>(y) + static_cast<size_t>(b) * outs * 2;
+    if (direct) continue;
     if (x_dtype == OC_DTYPE_BF16)
       hipLaunchKernelGGL(finish_kernel<OC_DTYPE_BF16>, dim3(grid_1d(outs)), dim3(256), 0, s, acc, C_out, L_out, bias,
                          bias_dtype, yb);

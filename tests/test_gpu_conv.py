@@ -117,7 +117,7 @@ def test_long_sequences_take_several_chunks():
     from onecomp_runtime.layers.packed_conv import conv1d_pads
 
     mod, (q, s, z, rows, cols) = _conv(PackedInt4Conv1d, 64, 96, 7, 14, 20700, pad_mode="auto")
-    B, L = 2, 40000  # 80000 output rows; a chunk holds 64 MB / (2 * 448 + 4 * 96) B = 52224 rows
+    B, L = 2, 60000  # 120000 output rows; a chunk holds 128 MB / (2 * 448 + 4 * 96) B = 104704 rows
     x = torch.randn(B, 64, L, generator=torch.Generator().manual_seed(9)).to(torch.bfloat16)
     say("conv1d long sequence")
     y = mod(x.to(DEV))
@@ -126,7 +126,7 @@ def test_long_sequences_take_several_chunks():
     assert y.shape == (B, 96, L + left + right - 6)
     assert_gemm_close(y, O.conv1d(np32(x), w, None, 1, 1, left, y.shape[-1], "bf16"), "conv1d long")
     tmod, (q, s, z, rows, cols) = _conv(PackedInt4ConvTranspose1d, 64, 96, 4, 8, 20701, stride=2, pad_mode="none")
-    Lt = 50000  # a chunk holds 64 MB / (2 * 64 + 4 * 384) B = 40320 positions
+    Lt = 100000  # a chunk holds 128 MB / (2 * 64 + 4 * 384) B = 80640 positions
     xt = torch.randn(1, 64, Lt, generator=torch.Generator().manual_seed(10)).to(torch.bfloat16)
     say("conv-transpose long sequence")
     yt = tmod(xt.to(DEV))
