@@ -416,6 +416,49 @@ size_t oc_rtn_conv1d_workspace_bytes(int32_t B, int32_t C_in, int32_t C_out,
                                      int32_t kernel_size, int32_t T_out);
 
 /*
+ * Load time, Conv1d (no reference counterpart: the reference dequantizes the
+ * weight for every call, layers/packed_conv.py:196-222): the RTN rows
+ * [N = C_out, row_bytes] (K = C_in * kernel_size codes each) re-laid for the
+ * large-M GEMM kernel, tiles of 16 output columns:
+ *   qt[((t * KS + ks) * 16 + c) * 4 + w]  codes of K rows 32 ks + 8 w .. + 7
+ *                                         of column 16 t + c (KS = K / 32)
+ *   sz[(t * G + g) * 16 + c]              scale | zero << 16 (16-bit values)
+ * with ceil(N / 16) tiles (columns past N zero): qt holds tiles * KS * 64 and
+ * sz tiles * G * 16 32-bit words (qt 16-byte aligned). fast[0] / fast[1]
+ * (device int32[2]) become 1 when every group's (scale, zero) allows the
+ * exact single-rounding dequant for bf16 / fp16 activations (an integral
+ * zero of magnitude <= 240 and a scale in (2^-100, 2^100) after rounding to
+ * that dtype), else 0. Needs K % 32 == 0, K / G % 32 == 0, row_bytes % 4 == 0,
+ * scales and zeros [N, G] of one 16-bit dtype.
+ */
+int oc_rtn_tile_prepare(const uint8_t *qweight, int32_t N, int32_t row_bytes,
+                        int32_t K, const void *scales, const void *zeros,
+                        int32_t dtype, int32_t G, int32_t *qt, uint32_t *sz,
+                        int32_t *fast, void *stream);
+
+/*
+ * oc_rtn_conv1d with the tile layout of the same weight (oc_rtn_tile_prepare;
+ * the reference interface is the one oc_rtn_conv1d cites). Chunks of 1024 or
+ * more output rows run on the large-M kernel when tiles_fast (the flag
+ * oc_rtn_tile_prepare reported for x_dtype) is nonzero, the group size is 32
+ * times a power of two, C_out % 8 == 0 and scales / zeros share a 16-bit
+ * dtype; other chunks, or qt / sz NULL, as oc_rtn_conv1d. Same workspace.
+ * Results match oc_rtn_conv1d to fp32 summation order (one-hot products
+ * bit-identical).
+ */
+int oc_rtn_conv1d_prepared(const void *x, int32_t x_dtype, int32_t B,
+                           int32_t C_in, int32_t L, const uint8_t *qweight,
+                           int32_t row_bytes, const void *scales,
+                           int32_t scale_dtype, const void *zeros,
+                           int32_t zero_dtype, int32_t G, const int32_t *qt,
+                           const uint32_t *sz, int32_t tiles_fast,
+                           int32_t C_out, int32_t kernel_size, int32_t stride,
+                           int32_t dilation, int32_t pad_left, int32_t T_out,
+                           const void *bias, int32_t bias_dtype, void *y,
+                           void *workspace, size_t workspace_bytes,
+                           void *stream);
+
+/*
  * Load time, ConvTranspose1d: the stored weight [rows = C_in, cols =
  * C_out * kernel_size] (quant groups along cols) re-laid as
  * qweight_t [cols, rows / 2] (RTN nibbles along C_in) and scales_t /

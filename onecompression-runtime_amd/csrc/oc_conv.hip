@@ -292,6 +292,67 @@ __global__ __launch_bounds__(256) void zero_f32_kernel(float *__restrict__ p, in
   if (idx < n) p[idx] = 0.f;
 }
 
+// RTN rows -> the large-M kernel's tiles (tile16 words): word (t, ks, c, w)
+// = codes of K rows 32 ks + 8 w .. + 7 of output column 16 t + c, which in
+// an RTN row are 4 consecutive bytes (code i at bits 4 i either way).
+__global__ __launch_bounds__(256) void rtn_tile_words_kernel(const uint8_t *__restrict__ q, int N, int row_bytes,
+                                                             int KS, int tiles, uint32_t *__restrict__ qt) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * KS * 64) return;
+  const int w = static_cast<int>(idx & 3), c = static_cast<int>((idx >> 2) & 15);
+  const int64_t tk = idx >> 6;
+  const int ks = static_cast<int>(tk % KS), n = static_cast<int>(tk / KS) * 16 + c;
+  qt[idx] = n < N ? *reinterpret_cast<const uint32_t *>(q + static_cast<int64_t>(n) * row_bytes + 16 * ks + 4 * w)
+                  : 0u;
+}
+
+__global__ void rtn_tile_flags_kernel(int *fast) {
+  if (threadIdx.x < 2) fast[threadIdx.x] = 1;
+}
+
+// Per (tile, group, column): scale | zero << 16 (16-bit values as stored;
+// columns past N zero). fast[0] / fast[1] are cleared when a column's group
+// parameter does not allow the exact single-rounding dequant for bf16 /
+// fp16 activations (rtn_fast_ok on the values rounded to that dtype).
+__global__ __launch_bounds__(256) void rtn_tile_params_kernel(const uint16_t *__restrict__ sc,
+                                                              const uint16_t *__restrict__ zr, int N, int G,
+                                                              int tiles, int sdt, uint32_t *__restrict__ sz,
+                                                              int *fast) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * G * 16) return;
+  const int c = static_cast<int>(idx & 15);
+  const int64_t tg = idx >> 4;
+  const int g = static_cast<int>(tg % G), n = static_cast<int>(tg / G) * 16 + c;
+  if (n >= N) {
+    sz[idx] = 0u;
+    return;
+  }
+  const uint32_t sv = sc[static_cast<int64_t>(n) * G + g], zv = zr[static_cast<int64_t>(n) * G + g];
+  sz[idx] = sv | zv << 16;
+  const float s = sdt == OC_DTYPE_BF16 ? half_to_f32<OC_DTYPE_BF16>(sv) : half_to_f32<OC_DTYPE_F16>(sv);
+  const float z = sdt == OC_DTYPE_BF16 ? half_to_f32<OC_DTYPE_BF16>(zv) : half_to_f32<OC_DTYPE_F16>(zv);
+  RtnParam pb, ph;
+  pb.sq = round_to<OC_DTYPE_BF16>(s);
+  pb.zq = round_to<OC_DTYPE_BF16>(z);
+  ph.sq = round_to<OC_DTYPE_F16>(s);
+  ph.zq = round_to<OC_DTYPE_F16>(z);
+  if (!rtn_fast_ok<OC_DTYPE_BF16>(pb)) atomicAnd(&fast[0], 0);
+  if (!rtn_fast_ok<OC_DTYPE_F16>(ph)) atomicAnd(&fast[1], 0);
+}
+
+// Large-M conv GEMM (the tiled RTN kernel below this many rows per chunk).
+constexpr int WIDE_CONV_MIN_ROWS = 1024;
+
+// K slices of the large-M kernel for a rows x N x K chunk: enough 256 x 192
+// workgroups to fill the compute units, each slice 16 K steps or more.
+int wide_conv_ksplit(int rows, int N, int K, int *kps) {
+  const int KS = K / 32;
+  const int wgs = ((N + 191) / 192) * ((rows + 255) / 256);
+  int ks = std::max(1, std::min(device_cus() / std::max(1, wgs), KS / 16));
+  *kps = (KS + ks - 1) / ks;
+  return (KS + *kps - 1) / *kps;
+}
+
 // Rows per chunk: a bounded workspace (activation rows plus fp32 partials),
 // the rows spread evenly over the chunks (multiples of 256), so that no
 // chunk is a small remainder whose GEMM fills a fraction of the chip.
@@ -306,10 +367,12 @@ int chunk_rows(int64_t total, int K, int N) {
   return static_cast<int>(std::min(r, rmax));
 }
 
-// Workspace of one chunk of `rows` rows: activations, then fp32 partials.
+// Workspace of one chunk of `rows` rows: activations, then fp32 partials
+// (as many K splits as the tiled or the large-M plan of the chunk takes).
 size_t chunk_bytes(int rows, int K, int N) {
   int wm, wn, kg, ksplit, kps;
   plan_tiled(rows, N, K, &wm, &wn, &kg, &ksplit, &kps);
+  if (rows >= WIDE_CONV_MIN_ROWS) ksplit = std::max(ksplit, wide_conv_ksplit(rows, N, K, &kps));
   const size_t a = (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256;
   return a + static_cast<size_t>(ksplit) * rows * N * sizeof(float);
 }
@@ -369,11 +432,46 @@ size_t oc_rtn_conv1d_workspace_bytes(int32_t B, int32_t C_in, int32_t C_out, int
   return conv_chunks_bytes(static_cast<int64_t>(B) * T_out, static_cast<int>(K), C_out);
 }
 
+int oc_rtn_tile_prepare(const uint8_t *qweight, int32_t N, int32_t row_bytes, int32_t K, const void *scales,
+                        const void *zeros, int32_t dtype, int32_t G, int32_t *qt, uint32_t *sz, int32_t *fast,
+                        void *stream) {
+  clear_error();
+  if (!qweight || !scales || !zeros || !qt || !sz || !fast) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (N <= 0 || K <= 0 || K % 32 != 0 || G <= 0 || K % G != 0 || (K / G) % 32 != 0 || row_bytes < K / 2 ||
+      row_bytes % 4 != 0)
+    return fail(OC_ERR_SHAPE, "tile layout needs K %% 32 == 0, groups of a multiple of 32 columns and 4-byte rows "
+                "(N=%d K=%d G=%d row_bytes=%d)", N, K, G, row_bytes);
+  if (dtype != OC_DTYPE_F16 && dtype != OC_DTYPE_BF16)
+    return fail(OC_ERR_INVALID_ARGUMENT, "scales and zeros must share a 16-bit dtype");
+  if (!aligned(qweight, 4)) return fail(OC_ERR_SHAPE, "misaligned weight");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int tiles = (N + 15) / 16, KS = K / 32;
+  hipLaunchKernelGGL(rtn_tile_words_kernel, dim3(grid_1d(static_cast<int64_t>(tiles) * KS * 64)), dim3(256), 0, s,
+                     qweight, N, row_bytes, KS, tiles, reinterpret_cast<uint32_t *>(qt));
+  hipLaunchKernelGGL(rtn_tile_flags_kernel, dim3(1), dim3(64), 0, s, fast);
+  hipLaunchKernelGGL(rtn_tile_params_kernel, dim3(grid_1d(static_cast<int64_t>(tiles) * G * 16)), dim3(256), 0, s,
+                     static_cast<const uint16_t *>(scales), static_cast<const uint16_t *>(zeros), N, G, tiles, dtype,
+                     sz, fast);
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
 int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32_t L, const uint8_t *qweight,
                   int32_t row_bytes, const void *scales, int32_t scale_dtype, const void *zeros, int32_t zero_dtype,
                   int32_t G, int32_t C_out, int32_t kernel_size, int32_t stride, int32_t dilation, int32_t pad_left,
                   int32_t T_out, const void *bias, int32_t bias_dtype, void *y, void *workspace,
                   size_t workspace_bytes, void *stream) {
+  return oc_rtn_conv1d_prepared(x, x_dtype, B, C_in, L, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype,
+                                G, nullptr, nullptr, 0, C_out, kernel_size, stride, dilation, pad_left, T_out, bias,
+                                bias_dtype, y, workspace, workspace_bytes, stream);
+}
+
+int oc_rtn_conv1d_prepared(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32_t L,
+                           const uint8_t *qweight, int32_t row_bytes, const void *scales, int32_t scale_dtype,
+                           const void *zeros, int32_t zero_dtype, int32_t G, const int32_t *qt, const uint32_t *sz,
+                           int32_t tiles_fast, int32_t C_out, int32_t kernel_size, int32_t stride, int32_t dilation,
+                           int32_t pad_left, int32_t T_out, const void *bias, int32_t bias_dtype, void *y,
+                           void *workspace, size_t workspace_bytes, void *stream) {
   clear_error();
   if (B < 0 || C_in <= 0 || L < 0 || C_out <= 0 || kernel_size <= 0 || stride <= 0 || dilation <= 0 || T_out < 0 ||
       G <= 0)
@@ -396,7 +494,16 @@ int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32
     return fail(OC_ERR_WORKSPACE, "workspace of %zu bytes required, %zu given", need,
                 workspace ? workspace_bytes : static_cast<size_t>(0));
   if (!aligned(workspace, 256) || !aligned(qweight, 4)) return fail(OC_ERR_SHAPE, "misaligned workspace or weight");
+  if ((qt && !aligned(qt, 16)) || (sz && !aligned(sz, 4))) return fail(OC_ERR_SHAPE, "misaligned tile layout");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The large-M kernel on the tile layout: 16-bit scales and zeros of one
+  // dtype, power-of-two group steps, every group fast-dequant eligible for
+  // x_dtype (tiles_fast, as oc_rtn_tile_prepare reported it); ONECOMP_HIP_CONV_WIDE=0
+  // (read per call; tests) keeps the tiled kernel.
+  const int gs = K / G;
+  const bool wide = qt && sz && tiles_fast && scale_dtype == zero_dtype && is_half_dtype(scale_dtype) &&
+                    gs % 32 == 0 && ilog2_exact(gs / 32) >= 0 && C_out % 8 == 0 &&
+                    env_int("ONECOMP_HIP_CONV_WIDE", 1) != 0;
   const int R = chunk_rows(total, K, C_out);
   for (int64_t r0 = 0; r0 < total; r0 += R) {
     const int rows = static_cast<int>(std::min<int64_t>(R, total - r0));
@@ -412,8 +519,31 @@ int oc_rtn_conv1d(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32
       hipLaunchKernelGGL(im2col_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * K)), dim3(256), 0, s,
                          static_cast<const uint16_t *>(x), C_in, L, kernel_size, stride, dilation, pad_left, T_out,
                          r0, rows, K, a);
-    const int ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype,
-                                  K / G, G, 1, C_out, false, part, s);
+    int ksplit;
+    if (wide && rows >= WIDE_CONV_MIN_ROWS && static_cast<int64_t>(rows) * K * 2 < (int64_t{1} << 31)) {
+      GemmParams p{};
+      p.a = a;
+      p.lda = K;
+      p.a_bytes = static_cast<int64_t>(rows) * K * 2;
+      p.M = rows;
+      p.K_logical = K;
+      p.qw = qt;
+      p.scales = sz;
+      p.N = C_out;
+      p.K_phys = K;
+      p.KS = K / 32;
+      p.G = G;
+      p.group_rows = gs;
+      p.gshift = ilog2_exact(gs / 32);
+      p.partials = part;
+      p.out_f32 = 1;
+      p.ksplit = wide_conv_ksplit(rows, C_out, K, &p.ksteps_per_split);
+      launch_rtn_wide(p, x_dtype, scale_dtype, s);
+      ksplit = p.ksplit;
+    } else {
+      ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype, K / G, G,
+                          1, C_out, false, part, s);
+    }
     const dim3 grid((rows + EP_R - 1) / EP_R, (C_out + EP_N - 1) / EP_N);
     if (x_dtype == OC_DTYPE_BF16)
       hipLaunchKernelGGL(conv1d_epilogue_tile_kernel<OC_DTYPE_BF16>, grid, dim3(256), 0, s, part, ksplit, rows, C_out,

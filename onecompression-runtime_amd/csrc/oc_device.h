@@ -257,6 +257,19 @@ __device__ __forceinline__ uint4 rtn_dequant8_fast(uint32_t q, RtnParam p) {
   return uint4{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3]), pack2<DT>(f[4], f[5]), pack2<DT>(f[6], f[7])};
 }
 
+// Codes 0-3 of q (bits 0-15) as rtn_dequant8_fast computes them, with
+// nzs = -zq * sq: returns {codes 0|1, codes 2|3}. Applied to q >> 16 it
+// yields codes 4-7.
+template <int DT>
+__device__ __forceinline__ uint2 rtn_fast_half(uint32_t q, float sq, float nzs) {
+  const uint32_t lo = q & 0x0F0Fu, hi = (q >> 4) & 0x0F0Fu;  // codes 0 2 | 1 3
+  const float f0 = __builtin_fmaf(static_cast<float>(lo & 0xFFu), sq, nzs);
+  const float f1 = __builtin_fmaf(static_cast<float>(hi & 0xFFu), sq, nzs);
+  const float f2 = __builtin_fmaf(static_cast<float>(lo >> 8), sq, nzs);
+  const float f3 = __builtin_fmaf(static_cast<float>(hi >> 8), sq, nzs);
+  return uint2{pack2<DT>(f0, f1), pack2<DT>(f2, f3)};
+}
+
 // ---- MFMA -----------------------------------------------------------------------
 //
 // v_mfma_f32_16x16x32_{bf16,f16} operand layout (one wave, lane l):

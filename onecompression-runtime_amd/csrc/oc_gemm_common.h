@@ -200,6 +200,8 @@ __device__ __forceinline__ uint4 octet_pairs(uint4 raw, float &sum) {
 
 // Host helpers.
 int env_int(const char *name, int dflt);
+int device_cus();          // compute units of the current device
+int ilog2_exact(int v);    // log2(v) for a power of two, else -1
 
 // LDS-tiled kernel over RTN nibble rows (oc_gemm.hip): tile shape and K split
 // for an M x N x K problem, and a launch of FMT_RTN (transposed = false) or
@@ -221,6 +223,10 @@ void launch_rows_gemv(const GemmParams &p, int x_dtype, int fmt, hipStream_t s);
 // Large-M kernel with 256-row wave tiles (oc_gemm_wide.hip): one launch over
 // ceil(M / 256) x ceil(N / (64 wn)) workgroups, wn = 3 or 4 tiles per wave.
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);
+// RTN tiles (oc_rtn_tile_prepare) on the large-M kernel into fp32 partials
+// [p.ksplit][M][N] (p.out_f32 = 1, p.partials); group steps a power of two
+// (p.gshift >= 0), N % 8 == 0, every group fast-dequant eligible.
+void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, hipStream_t s);
 
 // Decode GEMV over work items of T tiles x S K steps (oc_gemv.hip). K is split
 // into ksplit = ceil(KS / S) ranges; with ksplit > 1 the launch needs

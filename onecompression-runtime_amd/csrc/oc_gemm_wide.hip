@@ -21,6 +21,12 @@
 // per stage (lanes and waves without a job read out of the buffer range, which
 // returns zero, into a pad), and no other vector memory instruction runs in the
 // loop, so "this wave's copies of stage s+1 landed" is a fixed vmcnt.
+//
+// FMT_RTN (WN = 3): RTN codes re-laid into the same tiles (oc_rtn_tile_prepare)
+// with one word per (tile, group, column) holding the 16-bit scale and zero;
+// each code is the exact single-rounding value fma(code, sq, -zq sq) (the
+// host routes only layers whose every group allows it). A K split over
+// grid slices writes fp32 partials [split][M][N] for the caller's epilogue.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -43,13 +49,16 @@ constexpr int WIDE_NS = 4;  // LDS ring depth (stages), default
 //   WN = 3: 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 the scales
 //           (lanes 0-23) to S; 4-byte DMA: wave 0 the zero words (lanes 0-23),
 //           waves 1-3 a pad.
-template <int WN>
+//   RTN (WN = 3): 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 a pad
+//           (Z, 1 KB); 4-byte DMA: waves 0-2 copy the scale|zero words of
+//           tiles 4w..4w+3 to S + 64w (16 words per tile), wave 3 a pad.
+template <int WN, int FMT = FMT_GPTQ>
 struct WideLayout {
   static constexpr int TILES = 4 * WN;
   static constexpr int W = 0;
   static constexpr int S = 256 * WN;
-  static constexpr int Z = S + (WN == 4 ? 128 : 256);
-  static constexpr int P = Z + 64;
+  static constexpr int Z = S + (FMT == FMT_RTN ? 16 * TILES : WN == 4 ? 128 : 256);
+  static constexpr int P = Z + (FMT == FMT_RTN ? 256 : 64);
   static constexpr int DW = P + 64;
 };
 
@@ -57,10 +66,12 @@ struct WideLayout {
 // voffset + OOB_OFFSET stays below 2^32 because every voffset is below 2^31.
 constexpr uint32_t OOB_OFFSET = 0x80000000u;
 
-template <int DT, int SDT, int WN, int NS>
+template <int DT, int SDT, int WN, int NS, int FMT>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
-  using L = WideLayout<WN>;
+  using L = WideLayout<WN, FMT>;
+  constexpr bool RTN = FMT == FMT_RTN;
   static_assert(NS == 4 || NS == 6, "ring depth");
+  static_assert(FMT == FMT_GPTQ || (RTN && WN == 3), "formats");
   constexpr int BM = 256;
   constexpr int AST = BM * 4;  // uint4 per activation slot
   constexpr int DMA = 6;       // DMA instructions per wave and stage
@@ -95,16 +106,21 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   const int quad = lane >> 4, c16 = lane & 15;
   const int nbn = (p.N + 16 * L::TILES - 1) / (16 * L::TILES);
   const int nbm = (p.M + BM - 1) / BM;
-  const int flat = xcd_block(blockIdx.x, nbn * nbm);
-  const int bx = flat % nbn, by = flat / nbn;
+  // Workgroups of one K slice (RTN) and row block (they share activation
+  // rows) on one XCD.
+  const int flat = xcd_block(blockIdx.x, gridDim.x);
+  const int zs = RTN ? flat / (nbn * nbm) : 0, fl = flat - zs * (nbn * nbm);
+  const int bx = fl % nbn, by = fl / nbn;
   const int t0 = bx * L::TILES;
   const int m0 = by * BM;
   const int tiles = (p.N + TILE_N - 1) / TILE_N;
   const int KS = p.KS;
+  const int kb = RTN ? zs * p.ksteps_per_split : 0;              // this slice's first K step
+  const int nsteps = RTN ? min(KS - kb, p.ksteps_per_split) : KS;  // and its count (>= 1)
 
   const __amdgpu_buffer_rsrc_t rs_a = buffer_rsrc(p.a, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rs_q = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
-  const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * p.G * 32);
+  const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * p.G * (RTN ? 64 : 32));
   const __amdgpu_buffer_rsrc_t rs_z = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * p.G * 8);
 
   // Activation DMA i of wave w fills rows 16 (4w + i) + lane / 4 of the slot,
@@ -123,7 +139,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   uint32_t vo_x, vo_y;
   int x_kind, y_kind;  // 0: words, 1: scales, 2: zeros, 3: pad (soffset selector)
   int x_dst, y_dst;    // dword offsets in the slot
-  if (WN == 3 && wave == 3) {
+  if (RTN && wave == 3) {
+    rs_x = rs_q;
+    vo_x = OOB_OFFSET;
+    x_kind = 3;
+    x_dst = L::Z;
+  } else if (WN == 3 && wave == 3) {
     rs_x = rs_s;
     vo_x = lane < 24 ? static_cast<uint32_t>(tile_at(lane >> 1)) * p.G * 32 + 16 * (lane & 1) : OOB_OFFSET;
     x_kind = 1;
@@ -134,7 +155,13 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     x_kind = 0;
     x_dst = L::W + 256 * wave;
   }
-  if (WN == 4 && wave < 2) {
+  if (RTN) {
+    rs_y = rs_s;
+    vo_y = wave < 3 ? static_cast<uint32_t>(tile_at(4 * wave + (lane >> 4))) * p.G * 64 + 4 * (lane & 15)
+                    : OOB_OFFSET;
+    y_kind = wave < 3 ? 4 : 3;
+    y_dst = wave < 3 ? L::S + 64 * wave : L::P;
+  } else if (WN == 4 && wave < 2) {
     rs_y = rs_s;
     vo_y = static_cast<uint32_t>(tile_at(8 * wave + (lane >> 3))) * p.G * 32 + 4 * (lane & 7);
     y_kind = 1;
@@ -151,7 +178,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     y_dst = L::P;
   }
   auto soff = [&](int kind, int ks, int g) -> uint32_t {
-    return kind == 0 ? 256u * ks : kind == 1 ? 32u * g : kind == 2 ? 8u * g : 0u;
+    return kind == 0 ? 256u * ks : kind == 1 ? 32u * g : kind == 2 ? 8u * g : kind == 4 ? 64u * g : 0u;
   };
 
   // The copies of K step ks into one slot, one DMA instruction at a time
@@ -159,10 +186,11 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   // stage can spread them out. Past the end the activations read as zero
   // (out-of-range offset) and the weights repeat the last step, so the
   // padding steps of the last ring cycle add nothing.
+  // ks counts this slice's steps (K step kb + ks).
   auto issue_one = [&](uint4 *as, uint32_t *ws, int ks, int d) {
-    const int kk = min(ks, KS - 1);
+    const int kk = kb + min(ks, nsteps - 1);
     const int g = kk >> p.gshift;  // the host routes only power-of-two group steps here
-    if (d < 4) dma16(rs_a, avo[d], ks < KS ? 64u * ks : OOB_OFFSET, as + 64 * (4 * wave + d));
+    if (d < 4) dma16(rs_a, avo[d], ks < nsteps ? 64u * (kb + ks) : OOB_OFFSET, as + 64 * (4 * wave + d));
     else if (d == 4) dma16(rs_x, vo_x, soff(x_kind, kk, g), ws + x_dst);
     else dma4(rs_y, vo_y, soff(y_kind, kk, g), ws + y_dst);
   };
@@ -176,7 +204,8 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   // to land) and two sets of dequantized B operands.
   uint4 a[16], b0[WN], b1[WN];
 
-  // Weight words, scales and zero words of this wave's tiles for one stage.
+  // Weight words, scales and zero words of this wave's tiles for one stage
+  // (RTN: zw holds the column's scale | zero << 16).
   struct Meta {
     uint32_t q[WN], zw[WN];
     uint16_t sv[WN];
@@ -188,13 +217,31 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     for (int j = 0; j < WN; ++j) {
       const int tj = WN * wave + j;
       m.q[j] = ws[L::W + tj * 64 + c16 * 4 + quad];
-      m.sv[j] = sb[tj * 16 + c16];
-      m.zw[j] = ws[L::Z + tj * 2 + (c16 >> 3)];
+      if constexpr (RTN) {
+        m.zw[j] = ws[L::S + tj * 16 + c16];
+        m.sv[j] = 0;
+      } else {
+        m.sv[j] = sb[tj * 16 + c16];
+        m.zw[j] = ws[L::Z + tj * 2 + (c16 >> 3)];
+      }
     }
     return m;
   };
+  // RTN group parameter: s = RNE_DT(scale), c = -RNE_DT(zero) * s.
+  auto rtn_gp = [&](uint32_t w) {
+    GroupParam g{};
+    g.s = round_to<DT>(scale_f32<SDT>(w & 0xFFFFu));
+    g.c = -round_to<DT>(scale_f32<SDT>(w >> 16)) * g.s;
+    return g;
+  };
   auto dequant1 = [&](const Meta &m, int j) {
-    return dequant8<DT>(m.q[j], make_group_param(scale_f32<SDT>(m.sv[j]), tile_zero(m.zw[j], c16)));
+    if constexpr (RTN) {
+      const GroupParam g = rtn_gp(m.zw[j]);
+      const uint2 lo = rtn_fast_half<DT>(m.q[j], g.s, g.c), hi = rtn_fast_half<DT>(m.q[j] >> 16, g.s, g.c);
+      return uint4{lo.x, lo.y, hi.x, hi.y};
+    } else {
+      return dequant8<DT>(m.q[j], make_group_param(scale_f32<SDT>(m.sv[j]), tile_zero(m.zw[j], c16)));
+    }
   };  // (prologue)
   auto read_a = [&](const uint4 *as, int t) {
     const int row = 16 * t + c16;
@@ -245,7 +292,16 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
       const int part = t - 2;
       if (part >= 0 && part < PARTS) {
         const int j = part / 3;
-        if (part % 3 == 0) {
+        if constexpr (RTN) {
+          if (part % 3 == 0) {
+            gp[j] = rtn_gp(m.zw[j]);
+          } else if (part % 3 == 1) {
+            lo[j] = rtn_fast_half<DT>(m.q[j], gp[j].s, gp[j].c);  // codes 0-3
+          } else {
+            const uint2 hi = rtn_fast_half<DT>(m.q[j] >> 16, gp[j].s, gp[j].c);  // codes 4-7
+            bn[j] = uint4{lo[j].x, lo[j].y, hi.x, hi.y};
+          }
+        } else if (part % 3 == 0) {
           gp[j] = make_group_param(scale_f32<SDT>(m.sv[j]), tile_zero(m.zw[j], c16));
         } else if (part % 3 == 1) {
           lo[j] = dequant8_half<DT>(m.q[j], gp[j]);
@@ -282,7 +338,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   }
   // Whole ring cycles only (no remainder code: it would give the loop's
   // accumulators other registers and cost copies every iteration).
-  for (int s0 = 0; s0 < KS; s0 += NS) {
+  for (int s0 = 0; s0 < nsteps; s0 += NS) {
     step(ic<0>{}, s0);
     step(ic<1>{}, s0 + 1);
     step(ic<2>{}, s0 + 2);
@@ -296,6 +352,22 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   // four consecutive columns per lane, stored as one 8-byte write when the
   // output rows allow it (N is a multiple of 8, so a group of four is either
   // wholly inside N or wholly outside).
+  if constexpr (RTN) {
+    // fp32 partials of this K slice (N % 4 == 0: 16-byte stores), no bias.
+    float *part = p.partials + static_cast<int64_t>(zs) * p.M * p.N;
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n0 = TILE_N * (t0 + WN * wave + j) + 4 * quad;
+      if (n0 >= p.N) continue;
+#pragma unroll
+      for (int t = 0; t < 16; ++t) {
+        const int r = m0 + 16 * t + c16;
+        if (r >= p.M) continue;
+        const v4f32 v = acc[t][j];
+        *reinterpret_cast<float4 *>(part + static_cast<int64_t>(r) * p.N + n0) = make_float4(v[0], v[1], v[2], v[3]);
+      }
+    }
+  } else {
   const bool vec8 = ((reinterpret_cast<uintptr_t>(p.c) | static_cast<uintptr_t>(p.ldc * 2)) & 7) == 0;
 #pragma unroll
   for (int j = 0; j < WN; ++j) {
@@ -319,21 +391,39 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
       }
     }
   }
+  }
 }
 
 template <int DT, int SDT, int WN>
-static void launch_wide_t(const GemmParams &p, hipStream_t s) {
+static void launch_wide_t(const GemmParams &p_in, hipStream_t s) {  // GPTQ: bf16/fp16 output with bias
   // ONECOMP_HIP_WIDE_NS = 6 selects the 6-slot ring (tuning only).
   static const int ns = env_int("ONECOMP_HIP_WIDE_NS", WIDE_NS);
+  const GemmParams &p = p_in;
   const int nbn = (p.N + 64 * WN - 1) / (64 * WN), nbm = (p.M + 255) / 256;
-  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 6>), dim3(nbn * nbm), dim3(256), 0, s, p);
-  else hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 4>), dim3(nbn * nbm), dim3(256), 0, s, p);
+  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 6, FMT_GPTQ>), dim3(nbn * nbm), dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, WN, 4, FMT_GPTQ>), dim3(nbn * nbm), dim3(256), 0, s, p);
 }
 
 template <int DT, int SDT>
 static void launch_wide_d(const GemmParams &p, int wn, hipStream_t s) {
   if (wn == 3) launch_wide_t<DT, SDT, 3>(p, s);
   else launch_wide_t<DT, SDT, 4>(p, s);
+}
+
+// RTN tiles (WN = 3, 4-slot ring) into fp32 partials: p.ksplit slices of
+// p.ksteps_per_split K steps each.
+template <int DT, int SDT>
+static void launch_rtn_wide_t(const GemmParams &p, hipStream_t s) {
+  const int nbn = (p.N + 191) / 192, nbm = (p.M + 255) / 256;
+  hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 4, FMT_RTN>), dim3(nbn * nbm * p.ksplit), dim3(256), 0, s, p);
+}
+
+void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, hipStream_t s) {
+  const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
+  if (bf && sbf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, s);
+  else if (bf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_F16>(p, s);
+  else if (sbf) launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_BF16>(p, s);
+  else launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_F16>(p, s);
 }
 
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s) {

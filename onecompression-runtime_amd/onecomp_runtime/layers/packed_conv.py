@@ -147,6 +147,7 @@ class PackedInt4Conv1d(_PackedConvBase):
         super().__init__()
         self._init_common(in_channels, out_channels, kernel_size, stride, padding, dilation, groups, out_channels,
                           (in_channels // groups) * kernel_size, qweight, scales, zeros, cols, bias, causal, pad_mode)
+        self._tile_cache = None  # (key, qt, sz, fast flags): the large-M kernel's layout, built on first use
 
     def _materialize(self, dtype: torch.dtype) -> torch.Tensor:
         return self._dequant(dtype).reshape(self.out_channels, self.in_channels // self.groups, self.kernel_size)
@@ -156,6 +157,32 @@ class PackedInt4Conv1d(_PackedConvBase):
         return (x.is_cuda and x.dtype in (torch.float16, torch.bfloat16) and self.groups == 1 and x.dim() == 3
                 and K == self.in_channels * self.kernel_size and K % 32 == 0 and K % G == 0 and (K // G) % 8 == 0
                 and self.qweight.shape[1] % 4 == 0 and self.qweight.is_cuda)
+
+    def _tiles(self, x: torch.Tensor, rows: int):
+        """(qt, sz, fast) of the large-M kernel's layout (oc_rtn_tile_prepare),
+        built on the first call with enough output rows for it (1024) and
+        cached until the weight tensors change; (None, None, 0) where the
+        layout does not apply."""
+        K, G = self.cols, self.scales.shape[1]
+        gs = K // G
+        if (rows < 1024 or self.scales.dtype != self.zeros.dtype
+                or self.scales.dtype not in (torch.float16, torch.bfloat16) or gs % 32 != 0
+                or (gs // 32) & (gs // 32 - 1) != 0 or self.out_channels % 8 != 0):
+            return None, None, 0
+        key = tuple((t.data_ptr(), t._version) for t in (self.qweight, self.scales, self.zeros))
+        if self._tile_cache is None or self._tile_cache[0] != key:
+            N, tiles, dev = self.out_channels, (self.out_channels + 15) // 16, self.qweight.device
+            qt = torch.empty(tiles * (K // 32) * 64, dtype=torch.int32, device=dev)
+            sz = torch.empty(tiles * G * 16, dtype=torch.int32, device=dev)
+            fast = torch.empty(2, dtype=torch.int32, device=dev)
+            check(lib().oc_rtn_tile_prepare(ptr(self.qweight), N, self.qweight.shape[1], K,
+                                            ptr(self.scales.contiguous()), ptr(self.zeros.contiguous()),
+                                            dtype_code(self.scales.dtype), G, ptr(qt), ptr(sz), ptr(fast),
+                                            _hip.stream_of(dev)),
+                  "oc_rtn_tile_prepare")
+            self._tile_cache = (key, qt, sz, tuple(int(v) for v in fast.cpu()))
+        _, qt, sz, fast = self._tile_cache
+        return qt, sz, fast[0 if x.dtype == torch.bfloat16 else 1]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not x.is_cuda:
@@ -173,14 +200,17 @@ class PackedInt4Conv1d(_PackedConvBase):
         y = torch.empty((B, self.out_channels, max(T, 0)), dtype=x.dtype, device=x.device)
         if T <= 0:
             return y
+        qt, sz, fast = self._tiles(x, B * T)
         nbytes = int(lib().oc_rtn_conv1d_workspace_bytes(B, C, self.out_channels, self.kernel_size, T))
         ws, nbytes, stream = self._workspace(x.device, nbytes)
-        check(lib().oc_rtn_conv1d(ptr(x), dtype_code(x.dtype), B, C, L, ptr(self.qweight), self.qweight.shape[1],
-                                  ptr(self.scales), dtype_code(self.scales.dtype), ptr(self.zeros),
-                                  dtype_code(self.zeros.dtype), self.scales.shape[1], self.out_channels,
-                                  self.kernel_size, self.stride, self.dilation, left + self.padding, T, ptr(bias),
-                                  dtype_code(bias.dtype) if bias is not None else 0, ptr(y), ws, nbytes, stream),
-              "oc_rtn_conv1d")
+        check(lib().oc_rtn_conv1d_prepared(ptr(x), dtype_code(x.dtype), B, C, L, ptr(self.qweight),
+                                           self.qweight.shape[1], ptr(self.scales), dtype_code(self.scales.dtype),
+                                           ptr(self.zeros), dtype_code(self.zeros.dtype), self.scales.shape[1],
+                                           ptr(qt), ptr(sz), fast, self.out_channels, self.kernel_size, self.stride,
+                                           self.dilation, left + self.padding, T, ptr(bias),
+                                           dtype_code(bias.dtype) if bias is not None else 0, ptr(y), ws, nbytes,
+                                           stream),
+              "oc_rtn_conv1d_prepared")
         return y
 
     def extra_repr(self) -> str:

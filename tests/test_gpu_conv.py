@@ -71,6 +71,68 @@ def test_conv1d_one_hot_bit_exact_and_random(case):
     assert_gemm_close(mod_b(xr.to(DEV)), ref, f"conv1d case {case}")
 
 
+WIDE_CASES = [  # cin, cout, k, G, scale dtype: chunks of >= 1024 rows on the large-M kernel (K slices: 1, 2, 3)
+    (64, 200, 5, 5, np.float16),
+    (256, 200, 4, 8, np.float16),
+    (320, 96, 5, 25, "bf16"),
+]
+
+
+@pytest.mark.parametrize("case", range(len(WIDE_CASES)))
+def test_conv1d_large_m_kernel(case, monkeypatch):
+    """Conv1d chunks of 1024 or more rows on the tile layout (oc_rtn_tile_prepare
+    + the large-M kernel, K slices into fp32 partials): one-hot bit-exact,
+    random inputs at GEMM tolerance against the oracle and the tiled kernel;
+    non-integral zeros clear the fast flags and keep the tiled kernel."""
+    from onecomp_runtime.layers import PackedInt4Conv1d
+
+    cin, cout, k, G, sdt = WIDE_CASES[case]
+    cols = cin * k
+    q, s, z = _weights(cout, cols, G, 20900 + case)
+    if sdt == "bf16":
+        s_t = torch.from_numpy(s.astype(np.float32)).to(torch.bfloat16)
+        z_t = torch.from_numpy(z.astype(np.float32)).to(torch.bfloat16)
+        s32, z32 = s_t.float().numpy(), z_t.float().numpy()
+    else:
+        s_t, z_t = torch.from_numpy(s), torch.from_numpy(z)
+        s32, z32 = s.astype(np.float32), z.astype(np.float32)
+    bias = torch.randn(cout, generator=torch.Generator().manual_seed(case))
+    mod = PackedInt4Conv1d(cin, cout, k, qweight=torch.from_numpy(q), scales=s_t, zeros=z_t, cols=cols, bias=bias,
+                           pad_mode="none").to(DEV)
+    w = O.rtn_dequant(q, s32, z32, cols, cout, "bf16").reshape(cout, cin, k)
+    B, L = 2, 700
+    T = L - k + 1
+    x = torch.zeros(B, cin, L, dtype=torch.bfloat16)
+    x[0, 3, 17] = 1.0
+    x[1, cin - 1, L - 1] = 1.0
+    x[1, cin // 2, 400] = 1.0
+    xr = torch.randn(B, cin, L, generator=torch.Generator().manual_seed(30 + case)).to(torch.bfloat16)
+    ref = O.conv1d(np32(xr), w, O.round_to(bias.numpy(), "bf16"), 1, 1, 0, T, "bf16")
+    say(f"conv1d large-M kernel case {case}")
+    mod0 = PackedInt4Conv1d(cin, cout, k, qweight=torch.from_numpy(q), scales=s_t, zeros=z_t, cols=cols,
+                            pad_mode="none").to(DEV)
+    y1 = mod0(x.to(DEV))
+    assert mod0._tile_cache is not None and mod0._tile_cache[3] == (1, 1)
+    ref1 = O.conv1d(np32(x), w, None, 1, 1, 0, T, "bf16")
+    assert np.array_equal(bits16(y1), oracle_bits(ref1, torch.bfloat16))
+    yr = mod(xr.to(DEV))
+    assert_gemm_close(yr, ref, f"conv1d large-M case {case}")
+    monkeypatch.setenv("ONECOMP_HIP_CONV_WIDE", "0")
+    yt = mod(xr.to(DEV))
+    monkeypatch.delenv("ONECOMP_HIP_CONV_WIDE")
+    assert_gemm_close(yr, yt.float().cpu().numpy(), f"conv1d large-M vs tiled case {case}")
+    if case == 0:
+        zh = (z.astype(np.float32) + 0.5).astype(np.float16)
+        modh = PackedInt4Conv1d(cin, cout, k, qweight=torch.from_numpy(q), scales=s_t, zeros=torch.from_numpy(zh),
+                                cols=cols, bias=bias, pad_mode="none").to(DEV)
+        say("conv1d large-M kernel, half-integral zeros (tiled kernel)")
+        yh = modh(xr.to(DEV))
+        assert modh._tile_cache[3] == (0, 0)
+        wh = O.rtn_dequant(q, s32, zh.astype(np.float32), cols, cout, "bf16").reshape(cout, cin, k)
+        assert_gemm_close(yh, O.conv1d(np32(xr), wh, O.round_to(bias.numpy(), "bf16"), 1, 1, 0, T, "bf16"),
+                          "conv1d half-integral zeros")
+
+
 TCONV_CASES = [  # cin, cout, k, stride, dilation, padding, output_padding, pad_mode, causal, G
     (64, 48, 4, 2, 1, 0, 0, "auto", False, 6),
     (32, 40, 16, 8, 1, 0, 0, "auto", True, 1),
