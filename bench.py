@@ -435,9 +435,20 @@ def next_rows_workload(dev, steps, warmup):
         with torch.no_grad():
             y = mod(x)
             ms = graph_ms([lambda: mod(x)] * 4)
+            # The reference's forward on this GPU (layers/packed_conv.py:196-222): the weight dequantized on
+            # every call, then the library convolution; and the library convolution alone on a bf16 weight.
+            wd = mod._materialize(torch.bfloat16)
+            if cls is PackedInt4Conv1d:
+                conv = lambda w: torch.nn.functional.conv1d(x, w, None, 1, kw["padding"])
+            else:
+                conv = lambda w: torch.nn.functional.conv_transpose1d(x, w, None, kw["stride"])
+            ref_ms = time_ms(lambda i: conv(mod._materialize(torch.bfloat16)), 20, 3)
+            lib_ms = time_ms(lambda i: conv(wd), 20, 3)
+            del wd
         flops = 2 * cin * cout * k * (y.shape[-1] if cls is PackedInt4Conv1d else L)
         res[name] = {"us": ms * 1e3, "TFLOPs": flops / (ms * 1e-3) / 1e12,
-                     "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS}
+                     "mfma_frac": flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS,
+                     "reference_path_us": ref_ms * 1e3, "bf16_library_conv_us": lib_ms * 1e3}
     return res
 
 

@@ -70,6 +70,27 @@ __global__ __launch_bounds__(256) void im2col_tile_kernel(const uint16_t *__rest
     __syncthreads();
   }
   const int CH = I2C_CB * k / 8;  // 16-byte chunks of one row in this channel block
+  if (one_batch && CH <= 256) {
+    // A thread keeps one chunk column j (its 8 window offsets computed once)
+    // and walks the rows 256 / CH apart.
+    const int RS = 256 / CH, j = threadIdx.x % CH;
+    if (threadIdx.x >= RS * CH) return;
+    int off[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int cc = 8 * j + e, ci = cc / k;
+      off[e] = ci * W + (cc - ci * k) * dilation;
+    }
+    uint16_t *dst = a + (ra - r0) * K + static_cast<int64_t>(ci0) * k + 8 * j;
+    for (int rr = threadIdx.x / CH; rr < nrow; rr += RS) {
+      uint32_t v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = win[off[e] + rr * stride];
+      *reinterpret_cast<uint4 *>(dst + static_cast<int64_t>(rr) * K) =
+          make_uint4(v[0] | v[1] << 16, v[2] | v[3] << 16, v[4] | v[5] << 16, v[6] | v[7] << 16);
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < nrow * CH; i += blockDim.x) {
     const int rr = i / CH, j = i - rr * CH;
     const int64_t r = ra + rr;
@@ -207,7 +228,7 @@ __global__ __launch_bounds__(256) void col2im_add_kernel(const float *__restrict
 // read into LDS along the GEMM's columns, then each output adds its taps (kk
 // ascending, as above). FINAL (one chunk covers the whole input): the output
 // is written directly with the bias, rounded once (no accumulator pass).
-constexpr int CT_T = 64, CT_O = 16;
+constexpr int CT_T = 128, CT_O = 16;
 __host__ __device__ inline int floor_div(int a, int b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 inline int col2im_rows(int k, int stride, int dilation) { return (CT_T - 1 + (k - 1) * dilation) / stride + 2; }
 
@@ -217,15 +238,48 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
                                                           int t_lo, int t_hi, int Lout, int JR,
                                                           float *__restrict__ acc, const void *bias, int bias_dtype,
                                                           void *__restrict__ y) {
-  extern __shared__ float zs[];  // [JR][CT_O * k]
+  extern __shared__ __attribute__((aligned(16))) float zs[];  // [JR][CT_O * k]
   const int t0 = t_lo + static_cast<int>(blockIdx.x) * CT_T, o0 = static_cast<int>(blockIdx.y) * CT_O;
   const int N = O * k, W = CT_O * k;
   const int wlim = min(W, (O - o0) * k);  // columns of the tile's channels that exist
   const int64_t mn = static_cast<int64_t>(rows) * N;
   const int jlo = floor_div(t0 + padding - (k - 1) * dilation, stride);  // first input position reaching the tile
   const int total = JR * W;
-  // U independent loads per thread in flight (one chain per element).
+  // U independent loads per thread in flight (one chain per element); with
+  // N % 4 == 0 (then the tile's columns are whole 16-byte runs: o0 k and the
+  // existing width N - o0 k are multiples of 4) as 16-byte loads.
   constexpr int U = 4;
+  if ((N & 3) == 0) {
+    const int W4 = W >> 2, tot4 = total >> 2;
+    for (int i0 = threadIdx.x; i0 < tot4; i0 += U * 256) {
+      int64_t e[U];
+      float4 v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int i = i0 + u * 256;
+        const int jj = i / W4, c = 4 * (i - jj * W4);
+        const int j = jlo + jj - j0;
+        e[u] = i < tot4 && j >= 0 && j < rows && c < wlim
+                   ? static_cast<int64_t>(j) * N + static_cast<int64_t>(o0) * k + c
+                   : -1;
+        v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      for (int sp = 0; sp < ksplit; ++sp) {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (e[u] >= 0) {
+            const float4 t = *reinterpret_cast<const float4 *>(part + sp * mn + e[u]);
+            v[u].x += t.x;
+            v[u].y += t.y;
+            v[u].z += t.z;
+            v[u].w += t.w;
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (i0 + u * 256 < tot4) reinterpret_cast<float4 *>(zs)[i0 + u * 256] = v[u];
+    }
+  } else
   for (int i0 = threadIdx.x; i0 < total; i0 += U * 256) {
     int64_t e[U];
     float v[U];
