@@ -494,6 +494,51 @@ size_t oc_rtn_conv_transpose1d_workspace_bytes(int32_t B, int32_t C_in,
                                                int32_t L_out);
 
 /*
+ * Load time, ConvTranspose1d (no reference counterpart, as
+ * oc_rtn_tile_prepare): the stored weight [K = C_in rows, N = C_out *
+ * kernel_size cols] (quant groups along the cols) re-laid for the large-M
+ * kernel with activations of x_dtype:
+ *   qt[((t * KS + ks) * 16 + c) * 4 + w]  codes of rows 32 ks + 8 w .. + 7 of
+ *                                         column 16 t + c (KS = K / 32)
+ *   szt[t * K + row]                      sq | zq << 16: the row's scale and
+ *                                         zero for the tile's column group,
+ *                                         rounded to x_dtype (its bits)
+ * with ceil(N / 16) tiles (past N zero): tiles * KS * 64 and tiles * K 32-bit
+ * words, both 16-byte aligned. fast[0] (device int32) becomes 1 when every
+ * (scale, zero) allows the exact single-rounding dequant for x_dtype, else 0.
+ * Needs K % 32 == 0, N / G a multiple of 16, scales / zeros [K, G] of one
+ * 16-bit dtype.
+ */
+int oc_rtn_tile_prepare_t(const uint8_t *qweight, int32_t K,
+                          int32_t row_bytes, int32_t N, const void *scales,
+                          const void *zeros, int32_t scale_dtype, int32_t G,
+                          int32_t x_dtype, int32_t *qt, uint32_t *szt,
+                          int32_t *fast, void *stream);
+
+/*
+ * oc_rtn_conv_transpose1d with the transposed tile layout of the same weight
+ * (oc_rtn_tile_prepare_t for x_dtype; the reference interface is the one
+ * oc_rtn_conv_transpose1d cites). Chunks of 1024 or more input positions run
+ * their GEMM on the large-M kernel when tiles_fast (the flag the prepare step
+ * reported) is nonzero and C_out * kernel_size % 8 == 0; other chunks, or qt
+ * / szt NULL, as oc_rtn_conv_transpose1d. Same workspace. Results match it to
+ * fp32 summation order (one-hot inputs bit-identical).
+ */
+int oc_rtn_conv_transpose1d_prepared(const void *x, int32_t x_dtype, int32_t B,
+                                     int32_t C_in, int32_t L_in,
+                                     const uint8_t *qweight_t,
+                                     const void *scales_t, const void *zeros_t,
+                                     int32_t scale_dtype, int32_t G,
+                                     const int32_t *qt, const uint32_t *szt,
+                                     int32_t tiles_fast, int32_t C_out,
+                                     int32_t kernel_size, int32_t stride,
+                                     int32_t dilation, int32_t padding,
+                                     int32_t L_out, const void *bias,
+                                     int32_t bias_dtype, void *y,
+                                     void *workspace, size_t workspace_bytes,
+                                     void *stream);
+
+/*
  * Device: MoE routing prologue (no reference counterpart: the reference has
  * no grouped GEMM; its MoE path loops over experts, layers/dsv4_packed_linear.py:95-98).
  * Stable counting sort of the T*topk (token, slot) pairs by expert id:

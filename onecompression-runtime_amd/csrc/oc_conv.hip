@@ -190,14 +190,34 @@ __global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t *__rest
   out[idx] = in[static_cast<int64_t>(r) * G + g];
 }
 
-// A[j, ci] = x[b, ci, j0 + j] for the chunk's input positions.
-__global__ __launch_bounds__(256) void positions_to_rows_kernel(const uint16_t *__restrict__ x, int C, int L, int b,
-                                                                int j0, int rows, uint16_t *__restrict__ a) {
-  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (idx >= static_cast<int64_t>(rows) * C) return;
-  const int ci = static_cast<int>(idx % C);
-  const int j = static_cast<int>(idx / C);
-  a[idx] = x[(static_cast<int64_t>(b) * C + ci) * L + j0 + j];
+// A[j, ci] = x[b, ci, j0 + j] for the chunk's input positions, by 64 x 64
+// tiles through LDS: read along the positions, written as channel pairs
+// along the rows (C even), both coalesced.
+constexpr int PT = 64;
+__global__ __launch_bounds__(256) void positions_to_rows_tile_kernel(const uint16_t *__restrict__ x, int C, int L,
+                                                                     int b, int j0, int rows,
+                                                                     uint16_t *__restrict__ a) {
+  __shared__ uint16_t tile[PT][PT + 2];
+  const int jb = static_cast<int>(blockIdx.x) * PT, cb = static_cast<int>(blockIdx.y) * PT;
+  constexpr int NL = PT * PT / 256;  // loads per thread, all in flight
+  uint16_t v[NL];
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int i = threadIdx.x + 256 * u, cc = i / PT, jj = i % PT, ci = cb + cc, j = jb + jj;
+    v[u] = ci < C && j < rows ? x[(static_cast<int64_t>(b) * C + ci) * L + j0 + j] : static_cast<uint16_t>(0);
+  }
+#pragma unroll
+  for (int u = 0; u < NL; ++u) {
+    const int i = threadIdx.x + 256 * u;
+    tile[i / PT][i % PT] = v[u];
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < PT * PT / 2; i += 256) {
+    const int jj = i / (PT / 2), cp = 2 * (i % (PT / 2)), j = jb + jj, ci = cb + cp;
+    if (j < rows && ci < C)
+      *reinterpret_cast<uint32_t *>(a + static_cast<int64_t>(j) * C + ci) =
+          tile[cp][jj] | static_cast<uint32_t>(tile[cp + 1][jj]) << 16;
+  }
 }
 
 // acc[o, t] += taps of input positions j0 .. j0 + rows - 1, kk ascending, for
@@ -238,27 +258,34 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
                                                           int t_lo, int t_hi, int Lout, int JR,
                                                           float *__restrict__ acc, const void *bias, int bias_dtype,
                                                           void *__restrict__ y) {
-  extern __shared__ __attribute__((aligned(16))) float zs[];  // [JR][CT_O * k]
+  extern __shared__ __attribute__((aligned(16))) float zs[];  // [JR][CT_O * k + 8] (rows 8 floats apart
+                                                              // in bank: conflict-free tap reads)
+  __shared__ float bs[CT_O];                                  // the tile's biases
   const int t0 = t_lo + static_cast<int>(blockIdx.x) * CT_T, o0 = static_cast<int>(blockIdx.y) * CT_O;
   const int N = O * k, W = CT_O * k;
   const int wlim = min(W, (O - o0) * k);  // columns of the tile's channels that exist
   const int64_t mn = static_cast<int64_t>(rows) * N;
   const int jlo = floor_div(t0 + padding - (k - 1) * dilation, stride);  // first input position reaching the tile
-  const int total = JR * W;
+  const int total = JR * W, WS = W + 8;
+  if (FINAL && threadIdx.x < CT_O)
+    bs[threadIdx.x] = bias && o0 + static_cast<int>(threadIdx.x) < O ? load_any_f32(bias, o0 + threadIdx.x, bias_dtype)
+                                                                      : 0.f;
   // U independent loads per thread in flight (one chain per element); with
   // N % 4 == 0 (then the tile's columns are whole 16-byte runs: o0 k and the
   // existing width N - o0 k are multiples of 4) as 16-byte loads.
-  constexpr int U = 4;
+  constexpr int U = 8;
   if ((N & 3) == 0) {
     const int W4 = W >> 2, tot4 = total >> 2;
     for (int i0 = threadIdx.x; i0 < tot4; i0 += U * 256) {
       int64_t e[U];
+      int li[U];
       float4 v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = i0 + u * 256;
         const int jj = i / W4, c = 4 * (i - jj * W4);
         const int j = jlo + jj - j0;
+        li[u] = (jj * WS + c) >> 2;
         e[u] = i < tot4 && j >= 0 && j < rows && c < wlim
                    ? static_cast<int64_t>(j) * N + static_cast<int64_t>(o0) * k + c
                    : -1;
@@ -277,17 +304,19 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
       }
 #pragma unroll
       for (int u = 0; u < U; ++u)
-        if (i0 + u * 256 < tot4) reinterpret_cast<float4 *>(zs)[i0 + u * 256] = v[u];
+        if (i0 + u * 256 < tot4) reinterpret_cast<float4 *>(zs)[li[u]] = v[u];
     }
   } else
   for (int i0 = threadIdx.x; i0 < total; i0 += U * 256) {
     int64_t e[U];
+    int li[U];
     float v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int i = i0 + u * 256;
       const int jj = i / W, c = i - jj * W;
       const int j = jlo + jj - j0;  // row of the chunk
+      li[u] = jj * WS + c;
       e[u] = i < total && j >= 0 && j < rows && c < wlim ? static_cast<int64_t>(j) * N + static_cast<int64_t>(o0) * k + c
                                                           : -1;
       v[u] = 0.f;
@@ -299,7 +328,7 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
-      if (i0 + u * 256 < total) zs[i0 + u * 256] = v[u];
+      if (i0 + u * 256 < total) zs[li[u]] = v[u];
   }
   __syncthreads();
   const int dmax = (k - 1) * dilation;
@@ -319,10 +348,10 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
         if (d % dilation != 0) continue;
         kk = d / dilation;
       }
-      v += zs[(j - jlo) * W + ol * k + kk];
+      v += zs[(j - jlo) * WS + ol * k + kk];
     }
     if constexpr (FINAL) {
-      if (bias) v += load_any_f32(bias, o, bias_dtype);
+      if (bias) v += bs[ol];
       store_c<DT>(y, static_cast<int64_t>(o) * Lout + t, v);
     } else {
       acc[static_cast<int64_t>(o) * Lout + t] += v;
@@ -392,6 +421,51 @@ __global__ __launch_bounds__(256) void rtn_tile_params_kernel(const uint16_t *__
   ph.zq = round_to<OC_DTYPE_F16>(z);
   if (!rtn_fast_ok<OC_DTYPE_BF16>(pb)) atomicAnd(&fast[0], 0);
   if (!rtn_fast_ok<OC_DTYPE_F16>(ph)) atomicAnd(&fast[1], 0);
+}
+
+// A weight whose quant groups run along its columns ([K rows, N cols], the
+// ConvTranspose1d layout) -> the same tiles: word (t, ks, c, w) gathers the
+// codes of rows 32 ks + 8 w + i (i < 8, at bits 4 i) of column 16 t + c.
+__global__ __launch_bounds__(256) void rtnt_tile_words_kernel(const uint8_t *__restrict__ q, int row_bytes, int N,
+                                                              int KS, int tiles, uint32_t *__restrict__ qt) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * KS * 64) return;
+  const int w = static_cast<int>(idx & 3), c = static_cast<int>((idx >> 2) & 15);
+  const int64_t tk = idx >> 6;
+  const int ks = static_cast<int>(tk % KS), n = static_cast<int>(tk / KS) * 16 + c;
+  uint32_t v = 0;
+  if (n < N) {
+    const uint8_t *col = q + (n >> 1) + static_cast<int64_t>(32 * ks + 8 * w) * row_bytes;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v |= ((col[static_cast<int64_t>(i) * row_bytes] >> (4 * (n & 1))) & 0xFu) << (4 * i);
+  }
+  qt[idx] = v;
+}
+
+// Per (tile, K row): sq | zq << 16, the row's scale and zero for the tile's
+// column group (host: groups of a multiple of 16 columns) rounded to DT and
+// stored as DT bits; zero past N. fast[0] is cleared where rtn_fast_ok<DT>
+// fails.
+template <int DT>
+__global__ __launch_bounds__(256) void rtnt_tile_rows_kernel(const uint16_t *__restrict__ sc,
+                                                             const uint16_t *__restrict__ zr, int K, int N, int G,
+                                                             int tiles, int sdt, uint32_t *__restrict__ szt,
+                                                             int *fast) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= static_cast<int64_t>(tiles) * K) return;
+  const int row = static_cast<int>(idx % K), n0 = static_cast<int>(idx / K) * 16;
+  if (n0 >= N) {
+    szt[idx] = 0u;
+    return;
+  }
+  const int64_t e = static_cast<int64_t>(row) * G + n0 / (N / G);
+  const float s = sdt == OC_DTYPE_BF16 ? half_to_f32<OC_DTYPE_BF16>(sc[e]) : half_to_f32<OC_DTYPE_F16>(sc[e]);
+  const float z = sdt == OC_DTYPE_BF16 ? half_to_f32<OC_DTYPE_BF16>(zr[e]) : half_to_f32<OC_DTYPE_F16>(zr[e]);
+  RtnParam rp;
+  rp.sq = round_to<DT>(s);
+  rp.zq = round_to<DT>(z);
+  szt[idx] = pack2<DT>(rp.sq, rp.zq);
+  if (!rtn_fast_ok<DT>(rp)) atomicAnd(fast, 0);
 }
 
 // Large-M conv GEMM (the tiled RTN kernel below this many rows per chunk).
@@ -506,6 +580,32 @@ int oc_rtn_tile_prepare(const uint8_t *qweight, int32_t N, int32_t row_bytes, in
   hipLaunchKernelGGL(rtn_tile_params_kernel, dim3(grid_1d(static_cast<int64_t>(tiles) * G * 16)), dim3(256), 0, s,
                      static_cast<const uint16_t *>(scales), static_cast<const uint16_t *>(zeros), N, G, tiles, dtype,
                      sz, fast);
+  OC_RETURN_LAUNCH_STATUS();
+  return OC_OK;
+}
+
+int oc_rtn_tile_prepare_t(const uint8_t *qweight, int32_t K, int32_t row_bytes, int32_t N, const void *scales,
+                          const void *zeros, int32_t scale_dtype, int32_t G, int32_t x_dtype, int32_t *qt,
+                          uint32_t *szt, int32_t *fast, void *stream) {
+  clear_error();
+  if (!qweight || !scales || !zeros || !qt || !szt || !fast) return fail(OC_ERR_INVALID_ARGUMENT, "NULL pointer");
+  if (K <= 0 || K % 32 != 0 || N <= 0 || G <= 0 || N % G != 0 || (N / G) % 16 != 0 || row_bytes < (N + 1) / 2)
+    return fail(OC_ERR_SHAPE, "transposed tile layout needs K %% 32 == 0 and groups of a multiple of 16 columns "
+                "(K=%d N=%d G=%d row_bytes=%d)", K, N, G, row_bytes);
+  if (!is_half_dtype(scale_dtype) || !is_half_dtype(x_dtype))
+    return fail(OC_ERR_INVALID_ARGUMENT, "scales/zeros and activations must be F16 or BF16");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int tiles = (N + 15) / 16, KS = K / 32;
+  hipLaunchKernelGGL(rtnt_tile_words_kernel, dim3(grid_1d(static_cast<int64_t>(tiles) * KS * 64)), dim3(256), 0, s,
+                     qweight, row_bytes, N, KS, tiles, reinterpret_cast<uint32_t *>(qt));
+  hipLaunchKernelGGL(rtn_tile_flags_kernel, dim3(1), dim3(64), 0, s, fast);
+  const dim3 g(grid_1d(static_cast<int64_t>(tiles) * K));
+  if (x_dtype == OC_DTYPE_BF16)
+    hipLaunchKernelGGL(rtnt_tile_rows_kernel<OC_DTYPE_BF16>, g, dim3(256), 0, s, static_cast<const uint16_t *>(scales),
+                       static_cast<const uint16_t *>(zeros), K, N, G, tiles, scale_dtype, szt, fast);
+  else
+    hipLaunchKernelGGL(rtnt_tile_rows_kernel<OC_DTYPE_F16>, g, dim3(256), 0, s, static_cast<const uint16_t *>(scales),
+                       static_cast<const uint16_t *>(zeros), K, N, G, tiles, scale_dtype, szt, fast);
   OC_RETURN_LAUNCH_STATUS();
   return OC_OK;
 }
@@ -643,6 +743,18 @@ int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C
                             int32_t G, int32_t C_out, int32_t kernel_size, int32_t stride, int32_t dilation,
                             int32_t padding, int32_t L_out, const void *bias, int32_t bias_dtype, void *y,
                             void *workspace, size_t workspace_bytes, void *stream) {
+  return oc_rtn_conv_transpose1d_prepared(x, x_dtype, B, C_in, L_in, qweight_t, scales_t, zeros_t, scale_dtype, G,
+                                          nullptr, nullptr, 0, C_out, kernel_size, stride, dilation, padding, L_out,
+                                          bias, bias_dtype, y, workspace, workspace_bytes, stream);
+}
+
+int oc_rtn_conv_transpose1d_prepared(const void *x, int32_t x_dtype, int32_t B, int32_t C_in, int32_t L_in,
+                                     const uint8_t *qweight_t, const void *scales_t, const void *zeros_t,
+                                     int32_t scale_dtype, int32_t G, const int32_t *qt, const uint32_t *szt,
+                                     int32_t tiles_fast, int32_t C_out, int32_t kernel_size, int32_t stride,
+                                     int32_t dilation, int32_t padding, int32_t L_out, const void *bias,
+                                     int32_t bias_dtype, void *y, void *workspace, size_t workspace_bytes,
+                                     void *stream) {
   clear_error();
   if (B < 0 || C_in <= 0 || L_in < 0 || C_out <= 0 || kernel_size <= 0 || stride <= 0 || dilation <= 0 ||
       L_out < 0 || G <= 0 || padding < 0)
@@ -661,14 +773,21 @@ int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C
                 workspace ? workspace_bytes : static_cast<size_t>(0));
   if (!aligned(workspace, 256) || !aligned(qweight_t, 4) || !aligned(scales_t, 16) || !aligned(zeros_t, 16))
     return fail(OC_ERR_SHAPE, "misaligned workspace or weights");
+  if ((qt && !aligned(qt, 16)) || (szt && !aligned(szt, 16))) return fail(OC_ERR_SHAPE, "misaligned tile layout");
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // The large-M kernel on the transposed tile layout (prepared for x_dtype,
+  // tiles_fast as oc_rtn_tile_prepare_t reported it) for chunks of
+  // WIDE_CONV_MIN_ROWS or more positions; ONECOMP_HIP_CONV_WIDE=0 (read per
+  // call; tests) keeps the tiled kernel.
+  const bool wide = qt && szt && tiles_fast && (N / G) % 16 == 0 && N % 8 == 0 &&
+                    env_int("ONECOMP_HIP_CONV_WIDE", 1) != 0;
   float *acc = static_cast<float *>(workspace);
   char *chunk_ws = static_cast<char *>(workspace) + (static_cast<size_t>(C_out) * L_out * 4 + 255) / 256 * 256;
   const int R = chunk_rows(L_in, C_in, N);
   const int64_t outs = static_cast<int64_t>(C_out) * L_out;
   const int span_max = (R - 1) * stride + (kernel_size - 1) * dilation + 1;
   const int JR = col2im_rows(kernel_size, stride, dilation);
-  const size_t tile_lds = static_cast<size_t>(JR) * CT_O * kernel_size * 4;
+  const size_t tile_lds = static_cast<size_t>(JR) * (CT_O * kernel_size + 8) * 4;
   const bool tiled = tile_lds <= 48 * 1024;
   const bool direct = tiled && R >= L_in;  // one chunk: outputs written by the col2im pass itself
   const bool bf = x_dtype == OC_DTYPE_BF16;
@@ -679,10 +798,33 @@ int oc_rtn_conv_transpose1d(const void *x, int32_t x_dtype, int32_t B, int32_t C
       const int rows = std::min(R, L_in - j0);
       uint16_t *a = reinterpret_cast<uint16_t *>(chunk_ws);
       float *part = reinterpret_cast<float *>(chunk_ws + (static_cast<size_t>(rows) * C_in * 2 + 255) / 256 * 256);
-      hipLaunchKernelGGL(positions_to_rows_kernel, dim3(grid_1d(static_cast<int64_t>(rows) * C_in)), dim3(256), 0, s,
-                         static_cast<const uint16_t *>(x), C_in, L_in, b, j0, rows, a);
-      const int ksplit = chunk_gemm(a, x_dtype, rows, C_in, qweight_t, C_in / 2, scales_t, scale_dtype, zeros_t,
-                                    scale_dtype, N / G, 0, 0, N, true, part, s);
+      hipLaunchKernelGGL(positions_to_rows_tile_kernel, dim3((rows + PT - 1) / PT, (C_in + PT - 1) / PT), dim3(256), 0,
+                         s, static_cast<const uint16_t *>(x), C_in, L_in, b, j0, rows, a);
+      int ksplit;
+      if (wide && rows >= WIDE_CONV_MIN_ROWS) {
+        GemmParams p{};
+        p.a = a;
+        p.lda = C_in;
+        p.a_bytes = static_cast<int64_t>(rows) * C_in * 2;
+        p.M = rows;
+        p.K_logical = C_in;
+        p.qw = qt;
+        p.scales = szt;
+        p.N = N;
+        p.K_phys = C_in;
+        p.KS = C_in / 32;
+        p.G = 1;
+        p.group_rows = C_in;
+        p.gshift = 0;
+        p.partials = part;
+        p.out_f32 = 1;
+        p.ksplit = wide_conv_ksplit(rows, N, C_in, &p.ksteps_per_split);
+        launch_rtnt_wide(p, x_dtype, s);
+        ksplit = p.ksplit;
+      } else {
+        ksplit = chunk_gemm(a, x_dtype, rows, C_in, qweight_t, C_in / 2, scales_t, scale_dtype, zeros_t, scale_dtype,
+                            N / G, 0, 0, N, true, part, s);
+      }
       int t_lo = std::max(0, j0 * stride - padding);
       int t_hi = std::min(L_out, (j0 + rows - 1) * stride + (kernel_size - 1) * dilation - padding + 1);
       if (direct) {

@@ -25,8 +25,12 @@
 // FMT_RTN (WN = 3): RTN codes re-laid into the same tiles (oc_rtn_tile_prepare)
 // with one word per (tile, group, column) holding the 16-bit scale and zero;
 // each code is the exact single-rounding value fma(code, sq, -zq sq) (the
-// host routes only layers whose every group allows it). A K split over
-// grid slices writes fp32 partials [split][M][N] for the caller's epilogue.
+// host routes only layers whose every group allows it). FMT_RTN_T (WN = 3):
+// the same tiles of a weight whose quant groups run along the output columns
+// (ConvTranspose1d, oc_rtn_tile_prepare_t): one word per (tile, K row) holding
+// sq | zq << 16, already rounded to DT, so every code of a word has its own
+// row's parameters. A K split over grid slices writes fp32 partials
+// [split][M][N] for the caller's epilogue.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,15 +56,37 @@ constexpr int WIDE_NS = 4;  // LDS ring depth (stages), default
 //   RTN (WN = 3): 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 a pad
 //           (Z, 1 KB); 4-byte DMA: waves 0-2 copy the scale|zero words of
 //           tiles 4w..4w+3 to S + 64w (16 words per tile), wave 3 a pad.
+//   RTN_T (WN = 3): the 32 row words of each tile and K step at S + 32 tile:
+//           16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 the row
+//           words of tiles 0-7; 4-byte DMA: waves 0-1 those of tiles
+//           8+2w, 9+2w, waves 2-3 a pad.
 template <int WN, int FMT = FMT_GPTQ>
 struct WideLayout {
   static constexpr int TILES = 4 * WN;
   static constexpr int W = 0;
   static constexpr int S = 256 * WN;
-  static constexpr int Z = S + (FMT == FMT_RTN ? 16 * TILES : WN == 4 ? 128 : 256);
+  static constexpr int Z = S + (FMT == FMT_RTN ? 16 * TILES : FMT == FMT_RTN_T ? 32 * TILES : WN == 4 ? 128 : 256);
   static constexpr int P = Z + (FMT == FMT_RTN ? 256 : 64);
   static constexpr int DW = P + 64;
 };
+
+// Codes 0-3 of q (bits 0-15), code i with its K row's parameter word
+// pw[i] = sq | zq << 16 (DT bits): {codes 0|1, codes 2|3}, each
+// fma(code, sq, -zq sq) rounded once. Applied to q >> 16 with the next four
+// rows' words it yields codes 4-7.
+template <int DT>
+__device__ __forceinline__ uint2 rtnt_half(uint32_t q, uint4 pw) {
+  const uint32_t lo = q & 0x0F0Fu, hi = (q >> 4) & 0x0F0Fu;  // codes 0 2 | 1 3
+  const uint32_t w[4] = {pw.x, pw.y, pw.z, pw.w};
+  const uint32_t c[4] = {lo & 0xFFu, hi & 0xFFu, lo >> 8, hi >> 8};
+  float f[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float sq = half_to_f32<DT>(w[i] & 0xFFFFu);
+    f[i] = __builtin_fmaf(static_cast<float>(c[i]), sq, -half_to_f32<DT>(w[i] >> 16) * sq);
+  }
+  return uint2{pack2<DT>(f[0], f[1]), pack2<DT>(f[2], f[3])};
+}
 
 // A buffer offset no resource reaches (reads return zero, no memory access);
 // voffset + OOB_OFFSET stays below 2^32 because every voffset is below 2^31.
@@ -69,7 +95,8 @@ constexpr uint32_t OOB_OFFSET = 0x80000000u;
 template <int DT, int SDT, int WN, int NS, int FMT>
 __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   using L = WideLayout<WN, FMT>;
-  constexpr bool RTN = FMT == FMT_RTN;
+  constexpr bool RTNT = FMT == FMT_RTN_T;
+  constexpr bool RTN = FMT == FMT_RTN || RTNT;  // K slices, fp32 partials, wave 3's 16-byte job
   static_assert(NS == 4 || NS == 6, "ring depth");
   static_assert(FMT == FMT_GPTQ || (RTN && WN == 3), "formats");
   constexpr int BM = 256;
@@ -120,7 +147,9 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
 
   const __amdgpu_buffer_rsrc_t rs_a = buffer_rsrc(p.a, p.a_bytes);
   const __amdgpu_buffer_rsrc_t rs_q = buffer_rsrc(p.qw, static_cast<int64_t>(tiles) * KS * 256);
-  const __amdgpu_buffer_rsrc_t rs_s = buffer_rsrc(p.scales, static_cast<int64_t>(tiles) * p.G * (RTN ? 64 : 32));
+  const __amdgpu_buffer_rsrc_t rs_s =
+      buffer_rsrc(p.scales, RTNT ? static_cast<int64_t>(tiles) * p.K_phys * 4
+                                 : static_cast<int64_t>(tiles) * p.G * (RTN ? 64 : 32));
   const __amdgpu_buffer_rsrc_t rs_z = buffer_rsrc(p.zeros, static_cast<int64_t>(tiles) * p.G * 8);
 
   // Activation DMA i of wave w fills rows 16 (4w + i) + lane / 4 of the slot,
@@ -139,7 +168,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   uint32_t vo_x, vo_y;
   int x_kind, y_kind;  // 0: words, 1: scales, 2: zeros, 3: pad (soffset selector)
   int x_dst, y_dst;    // dword offsets in the slot
-  if (RTN && wave == 3) {
+  if (RTNT && wave == 3) {
+    rs_x = rs_s;
+    vo_x = static_cast<uint32_t>(tile_at(lane >> 3)) * p.K_phys * 4 + 16 * (lane & 7);
+    x_kind = 5;
+    x_dst = L::S;
+  } else if (RTN && wave == 3) {
     rs_x = rs_q;
     vo_x = OOB_OFFSET;
     x_kind = 3;
@@ -155,7 +189,13 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     x_kind = 0;
     x_dst = L::W + 256 * wave;
   }
-  if (RTN) {
+  if (RTNT) {
+    rs_y = rs_s;
+    vo_y = wave < 2 ? static_cast<uint32_t>(tile_at(8 + 2 * wave + (lane >> 5))) * p.K_phys * 4 + 4 * (lane & 31)
+                    : OOB_OFFSET;
+    y_kind = wave < 2 ? 5 : 3;
+    y_dst = wave < 2 ? L::S + 256 + 64 * wave : L::P;
+  } else if (RTN) {
     rs_y = rs_s;
     vo_y = wave < 3 ? static_cast<uint32_t>(tile_at(4 * wave + (lane >> 4))) * p.G * 64 + 4 * (lane & 15)
                     : OOB_OFFSET;
@@ -178,7 +218,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     y_dst = L::P;
   }
   auto soff = [&](int kind, int ks, int g) -> uint32_t {
-    return kind == 0 ? 256u * ks : kind == 1 ? 32u * g : kind == 2 ? 8u * g : kind == 4 ? 64u * g : 0u;
+    return kind == 0   ? 256u * ks
+           : kind == 1 ? 32u * g
+           : kind == 2 ? 8u * g
+           : kind == 4 ? 64u * g
+           : kind == 5 ? 128u * ks
+                       : 0u;
   };
 
   // The copies of K step ks into one slot, one DMA instruction at a time
@@ -209,6 +254,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   struct Meta {
     uint32_t q[WN], zw[WN];
     uint16_t sv[WN];
+    uint4 pw[RTNT ? WN : 1][2];  // RTN_T: the row words of the lane's 8 K rows per tile
   };
   auto read_meta = [&](const uint32_t *ws) {
     const uint16_t *sb = reinterpret_cast<const uint16_t *>(ws + L::S);
@@ -217,7 +263,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     for (int j = 0; j < WN; ++j) {
       const int tj = WN * wave + j;
       m.q[j] = ws[L::W + tj * 64 + c16 * 4 + quad];
-      if constexpr (RTN) {
+      if constexpr (RTNT) {
+        m.zw[j] = 0;
+        m.sv[j] = 0;
+        m.pw[j][0] = reinterpret_cast<const uint4 *>(ws + L::S + tj * 32 + 8 * quad)[0];
+        m.pw[j][1] = reinterpret_cast<const uint4 *>(ws + L::S + tj * 32 + 8 * quad)[1];
+      } else if constexpr (RTN) {
         m.zw[j] = ws[L::S + tj * 16 + c16];
         m.sv[j] = 0;
       } else {
@@ -235,7 +286,11 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     return g;
   };
   auto dequant1 = [&](const Meta &m, int j) {
-    if constexpr (RTN) {
+    if constexpr (RTNT) {
+      const uint2 lo = rtnt_half<DT>(m.q[j], m.pw[j][0]);
+      const uint2 hi = rtnt_half<DT>(m.q[j] >> 16, m.pw[j][1]);
+      return uint4{lo.x, lo.y, hi.x, hi.y};
+    } else if constexpr (RTN) {
       const GroupParam g = rtn_gp(m.zw[j]);
       const uint2 lo = rtn_fast_half<DT>(m.q[j], g.s, g.c), hi = rtn_fast_half<DT>(m.q[j] >> 16, g.s, g.c);
       return uint4{lo.x, lo.y, hi.x, hi.y};
@@ -292,7 +347,15 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
       const int part = t - 2;
       if (part >= 0 && part < PARTS) {
         const int j = part / 3;
-        if constexpr (RTN) {
+        if constexpr (RTNT) {
+          // (the row words arrive with the stage's metadata; part 0 idles)
+          if (part % 3 == 1) {
+            lo[j] = rtnt_half<DT>(m.q[j], m.pw[j][0]);  // codes 0-3
+          } else if (part % 3 == 2) {
+            const uint2 hi = rtnt_half<DT>(m.q[j] >> 16, m.pw[j][1]);  // codes 4-7
+            bn[j] = uint4{lo[j].x, lo[j].y, hi.x, hi.y};
+          }
+        } else if constexpr (RTN) {
           if (part % 3 == 0) {
             gp[j] = rtn_gp(m.zw[j]);
           } else if (part % 3 == 1) {
@@ -414,8 +477,25 @@ static void launch_wide_d(const GemmParams &p, int wn, hipStream_t s) {
 // p.ksteps_per_split K steps each.
 template <int DT, int SDT>
 static void launch_rtn_wide_t(const GemmParams &p, hipStream_t s) {
+  static const int ns = env_int("ONECOMP_HIP_RTN_WIDE_NS", WIDE_NS);
   const int nbn = (p.N + 191) / 192, nbm = (p.M + 255) / 256;
-  hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 4, FMT_RTN>), dim3(nbn * nbm * p.ksplit), dim3(256), 0, s, p);
+  const dim3 g(nbn * nbm * p.ksplit);
+  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 6, FMT_RTN>), g, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 4, FMT_RTN>), g, dim3(256), 0, s, p);
+}
+
+template <int DT>
+static void launch_rtnt_wide_t(const GemmParams &p, hipStream_t s) {
+  static const int ns = env_int("ONECOMP_HIP_RTN_WIDE_NS", WIDE_NS);
+  const int nbn = (p.N + 191) / 192, nbm = (p.M + 255) / 256;
+  const dim3 g(nbn * nbm * p.ksplit);
+  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 3, 6, FMT_RTN_T>), g, dim3(256), 0, s, p);
+  else hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 3, 4, FMT_RTN_T>), g, dim3(256), 0, s, p);
+}
+
+void launch_rtnt_wide(const GemmParams &p, int a_dtype, hipStream_t s) {
+  if (a_dtype == OC_DTYPE_BF16) launch_rtnt_wide_t<OC_DTYPE_BF16>(p, s);
+  else launch_rtnt_wide_t<OC_DTYPE_F16>(p, s);
 }
 
 void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, hipStream_t s) {

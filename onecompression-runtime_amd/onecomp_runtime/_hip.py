@@ -150,6 +150,12 @@ SIGNATURES = {
          _I32, _I32, _P, _I32, _P, _P, _SZ, _P],
     ),
     "oc_rtn_transpose_prepare": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _P, _P, _P, _P]),
+    "oc_rtn_tile_prepare_t": (ctypes.c_int, [_P, _I32, _I32, _I32, _P, _P, _I32, _I32, _I32, _P, _P, _P, _P]),
+    "oc_rtn_conv_transpose1d_prepared": (
+        ctypes.c_int,
+        [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _I32, _I32, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32,
+         _P, _I32, _P, _P, _SZ, _P],
+    ),
     "oc_rtn_conv_transpose1d": (
         ctypes.c_int,
         [_P, _I32, _I32, _I32, _I32, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _I32, _I32, _I32,

@@ -231,6 +231,7 @@ class PackedInt4ConvTranspose1d(_PackedConvBase):
                           (out_channels // groups) * kernel_size, qweight, scales, zeros, cols, bias, causal,
                           pad_mode)
         self._transposed = None  # (key, qweight_t, scales_t, zeros_t): the GEMM layout, built on first use
+        self._tile_cache = {}  # activation dtype -> (key, qt, szt, fast): the large-M kernel's layout
 
     def _materialize(self, dtype: torch.dtype) -> torch.Tensor:
         return self._dequant(dtype).reshape(self.in_channels, self.out_channels // self.groups, self.kernel_size)
@@ -257,6 +258,30 @@ class PackedInt4ConvTranspose1d(_PackedConvBase):
             self._transposed = (key, qt, st, zt)
         return self._transposed[1:]
 
+    def _tiles(self, x: torch.Tensor, positions: int):
+        """(qt, szt, fast) of the large-M kernel's layout for x's dtype
+        (oc_rtn_tile_prepare_t), built on the first call with 1024 or more
+        input positions and cached until the weight tensors change; (None,
+        None, 0) where the layout does not apply."""
+        N, G = self.cols, self.scales.shape[1]
+        if positions < 1024 or (N // G) % 16 != 0 or N % 8 != 0:
+            return None, None, 0
+        key = tuple((t.data_ptr(), t._version) for t in (self.qweight, self.scales, self.zeros))
+        hit = self._tile_cache.get(x.dtype)
+        if hit is None or hit[0] != key:
+            K, tiles, dev = self.in_channels, (N + 15) // 16, self.qweight.device
+            qt = torch.empty(tiles * (K // 32) * 64, dtype=torch.int32, device=dev)
+            szt = torch.empty(tiles * K, dtype=torch.int32, device=dev)
+            fast = torch.empty(1, dtype=torch.int32, device=dev)
+            check(lib().oc_rtn_tile_prepare_t(ptr(self.qweight), K, self.qweight.shape[1], N,
+                                              ptr(self.scales.contiguous()), ptr(self.zeros.contiguous()),
+                                              dtype_code(self.scales.dtype), G, dtype_code(x.dtype), ptr(qt),
+                                              ptr(szt), ptr(fast), _hip.stream_of(dev)),
+                  "oc_rtn_tile_prepare_t")
+            hit = (key, qt, szt, int(fast.cpu()[0]))
+            self._tile_cache[x.dtype] = hit
+        return hit[1], hit[2], hit[3]
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if not x.is_cuda:
             raise RuntimeError("PackedInt4ConvTranspose1d runs on the HIP device; there is no CPU fallback")
@@ -272,15 +297,17 @@ class PackedInt4ConvTranspose1d(_PackedConvBase):
         y = torch.empty((B, self.out_channels, max(L_out, 0)), dtype=x.dtype, device=x.device)
         if L_out > 0 and L > 0:
             qt, st, zt = self._gemm_layout()
+            wt, szt, fast = self._tiles(x, L)
             nbytes = int(lib().oc_rtn_conv_transpose1d_workspace_bytes(B, C, L, self.out_channels,
                                                                        self.kernel_size, L_out))
             ws, nbytes, stream = self._workspace(x.device, nbytes)
-            check(lib().oc_rtn_conv_transpose1d(ptr(x), dtype_code(x.dtype), B, C, L, ptr(qt), ptr(st), ptr(zt),
-                                                dtype_code(st.dtype), st.shape[0], self.out_channels,
-                                                self.kernel_size, self.stride, self.dilation, self.padding, L_out,
-                                                ptr(bias), dtype_code(bias.dtype) if bias is not None else 0, ptr(y),
-                                                ws, nbytes, stream),
-                  "oc_rtn_conv_transpose1d")
+            check(lib().oc_rtn_conv_transpose1d_prepared(ptr(x), dtype_code(x.dtype), B, C, L, ptr(qt), ptr(st),
+                                                         ptr(zt), dtype_code(st.dtype), st.shape[0], ptr(wt),
+                                                         ptr(szt), fast, self.out_channels, self.kernel_size,
+                                                         self.stride, self.dilation, self.padding, L_out, ptr(bias),
+                                                         dtype_code(bias.dtype) if bias is not None else 0, ptr(y),
+                                                         ws, nbytes, stream),
+                  "oc_rtn_conv_transpose1d_prepared")
         return _convtranspose1d_unpad(y, self.kernel_size, self.stride, self.pad_mode, self.causal)
 
     def extra_repr(self) -> str:

@@ -172,6 +172,65 @@ def test_conv_transpose1d_one_hot_bit_exact_and_random(case):
     assert_gemm_close(mod_b(xr.to(DEV)), ref, f"conv-transpose case {case}")
 
 
+TWIDE_CASES = [  # cin, cout, k, stride, G: 1024+ input positions on the large-M kernel (K slices: 1, 1, 2)
+    (64, 48, 4, 2, 6),
+    (128, 40, 16, 8, 20),
+    (512, 24, 8, 4, 6),
+]
+
+
+@pytest.mark.parametrize("case", range(len(TWIDE_CASES)))
+def test_conv_transpose1d_large_m_kernel(case, monkeypatch):
+    """ConvTranspose1d GEMMs over 1024 or more input positions on the
+    transposed tile layout (oc_rtn_tile_prepare_t: per-K-row parameters
+    rounded to the activation dtype, one layout per dtype): one-hot
+    bit-exact in bf16 and fp16, random inputs at GEMM tolerance against the
+    oracle and the tiled kernel; non-integral zeros keep the tiled kernel."""
+    from onecomp_runtime.layers import PackedInt4ConvTranspose1d
+
+    cin, cout, k, st, G = TWIDE_CASES[case]
+    cols = cout * k
+    q, s, z = _weights(cin, cols, G, 21000 + case)
+    bias = torch.randn(cout, generator=torch.Generator().manual_seed(case))
+    kw = dict(stride=st, pad_mode="none")
+    mod0 = PackedInt4ConvTranspose1d(cin, cout, k, qweight=torch.from_numpy(q), scales=torch.from_numpy(s),
+                                     zeros=torch.from_numpy(z), cols=cols, **kw).to(DEV)
+    mod = PackedInt4ConvTranspose1d(cin, cout, k, qweight=torch.from_numpy(q), scales=torch.from_numpy(s),
+                                    zeros=torch.from_numpy(z), cols=cols, bias=bias, **kw).to(DEV)
+    B, L = 1, 1100
+    L_out = (L - 1) * st + k
+    for tdt, odt in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        w = _wd(q, s, z, cols, cin, odt).reshape(cin, cout, k)
+        x = torch.zeros(B, cin, L, dtype=tdt)
+        x[0, 3, 10] = 1.0
+        x[0, cin - 1, L - 1] = 1.0
+        x[0, cin // 2, 700] = 1.0
+        say(f"conv-transpose large-M kernel case {case} {odt}")
+        y1 = mod0(x.to(DEV))
+        assert mod0._tile_cache[tdt][3] == 1
+        ref1 = O.conv_transpose1d(np32(x), w, None, st, 1, 0, L_out, odt)
+        assert np.array_equal(bits16(y1), oracle_bits(ref1, tdt))
+    w = _wd(q, s, z, cols, cin).reshape(cin, cout, k)
+    xr = torch.randn(B, cin, L, generator=torch.Generator().manual_seed(40 + case)).to(torch.bfloat16)
+    ref = O.conv_transpose1d(np32(xr), w, O.round_to(bias.numpy(), "bf16"), st, 1, 0, L_out, "bf16")
+    yr = mod(xr.to(DEV))
+    assert_gemm_close(yr, ref, f"conv-transpose large-M case {case}")
+    monkeypatch.setenv("ONECOMP_HIP_CONV_WIDE", "0")
+    yt = mod(xr.to(DEV))
+    monkeypatch.delenv("ONECOMP_HIP_CONV_WIDE")
+    assert_gemm_close(yr, yt.float().cpu().numpy(), f"conv-transpose large-M vs tiled case {case}")
+    if case == 0:
+        zh = (z.astype(np.float32) + 0.5).astype(np.float16)
+        modh = PackedInt4ConvTranspose1d(cin, cout, k, qweight=torch.from_numpy(q), scales=torch.from_numpy(s),
+                                         zeros=torch.from_numpy(zh), cols=cols, bias=bias, **kw).to(DEV)
+        say("conv-transpose large-M kernel, half-integral zeros (tiled kernel)")
+        yh = modh(xr.to(DEV))
+        assert modh._tile_cache[torch.bfloat16][3] == 0
+        wh = _wd(q, s, zh, cols, cin).reshape(cin, cout, k)
+        assert_gemm_close(yh, O.conv_transpose1d(np32(xr), wh, O.round_to(bias.numpy(), "bf16"), st, 1, 0, L_out,
+                                                 "bf16"), "conv-transpose half-integral zeros")
+
+
 def test_long_sequences_take_several_chunks():
     """More positions than one workspace chunk holds: chunked im2col rows for
     Conv1d, chunked input positions (accumulated in order) for the transpose."""
