@@ -122,7 +122,11 @@ __global__ __launch_bounds__(256) void conv1d_epilogue_tile_kernel(const float *
                                                                    const void *bias, int bias_dtype,
                                                                    void *__restrict__ y) {
   __shared__ float tile[EP_R][EP_N + 1];
+  __shared__ float bs[EP_N];  // the tile's biases (no global loads among the stores)
   const int rb = static_cast<int>(blockIdx.x) * EP_R, nb = static_cast<int>(blockIdx.y) * EP_N;
+  if (threadIdx.x < EP_N)
+    bs[threadIdx.x] = bias && nb + static_cast<int>(threadIdx.x) < N ? load_any_f32(bias, nb + threadIdx.x, bias_dtype)
+                                                                      : 0.f;
   const int64_t mn = static_cast<int64_t>(rows) * N;
   constexpr int U = EP_R * EP_N / 256;
   int64_t e[U];
@@ -152,7 +156,7 @@ __global__ __launch_bounds__(256) void conv1d_epilogue_tile_kernel(const float *
     const int i = threadIdx.x + 256 * u, nn = i / EP_R, rr = i % EP_R, n = nb + nn;
     if (rb + rr >= rows || n >= N) continue;
     float val = tile[rr][nn];
-    if (bias) val += load_any_f32(bias, n, bias_dtype);
+    if (bias) val += bs[nn];
     int t = t0 + rr;
     int64_t b = b0;
     while (t >= T) {  // rows of the tile past the end of a batch row

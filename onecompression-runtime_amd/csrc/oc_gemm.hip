@@ -385,6 +385,7 @@ __global__ __launch_bounds__(64 * NW) void gemv_mfma_kernel(GemmParams p) {
   }
   if (wave != 0 || n >= p.N) return;
   const float bv = bias_at(p, n);
+  wait_vmcnt<0>();  // the bias is in on every path: the stores below wait for nothing
 #pragma unroll
   for (int tt = 0; tt < MT; ++tt)
 #pragma unroll
@@ -455,10 +456,12 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(GemmParams p) {
     }
   }
   const int64_t o = static_cast<int64_t>(row) * p.ldc + n;
-  store_c<DT>(p.c, o, v.x + bias_at(p, n));
-  store_c<DT>(p.c, o + 1, v.y + bias_at(p, n + 1));
-  store_c<DT>(p.c, o + 2, v.z + bias_at(p, n + 2));
-  store_c<DT>(p.c, o + 3, v.w + bias_at(p, n + 3));
+  const float b0 = bias_at(p, n), b1 = bias_at(p, n + 1), b2 = bias_at(p, n + 2), b3 = bias_at(p, n + 3);
+  wait_vmcnt<0>();  // every bias in before the first store
+  store_c<DT>(p.c, o, v.x + b0);
+  store_c<DT>(p.c, o + 1, v.y + b1);
+  store_c<DT>(p.c, o + 2, v.z + b2);
+  store_c<DT>(p.c, o + 3, v.w + b3);
 }
 
 // ---------------------------------------------------------------------------
@@ -750,11 +753,21 @@ __global__ __launch_bounds__(256 * KG) void gemm_tiled_kernel(GemmParams p) {
   }
   // Epilogue. acc[t][j][i] = tile row 16t + 4*quad + i, column 16*(tw+j) + c16.
   if (p.ksplit == 1 && !p.out_f32) {
+    // Every bias first and one wait on every path: bias loads behind dtype
+    // branches mixed with the stores made the compiler wait for all memory
+    // operations, the previous stores included, before each store.
+    float bvs[WN];
+#pragma unroll
+    for (int j = 0; j < WN; ++j) {
+      const int n = TILE_N * (tw + j) + c16;
+      bvs[j] = n < p.N ? bias_at(p, n) : 0.f;
+    }
+    wait_vmcnt<0>();
 #pragma unroll
     for (int j = 0; j < WN; ++j) {
       const int n = TILE_N * (tw + j) + c16;
       if (n >= p.N) continue;
-      const float bv = bias_at(p, n);
+      const float bv = bvs[j];
 #pragma unroll
       for (int t = 0; t < WM; ++t)
 #pragma unroll
@@ -1019,18 +1032,33 @@ __global__ __launch_bounds__(256, MOE && NSX == 4 ? 3 : (WM <= 8 && WN == 3 && N
     // Epilogue. acc[t][j][i] = row m0 + 16t + 4*quad + i, column 16*(t0 + WN wave + j) + c16.
     const int tw = t0 + WN * wave;
     if (MOE || p.ksplit == 1) {
+      // Biases first, then per row tile its destination rows (grouped: loads
+      // of the routing table), each time one wait on every path (loads mixed
+      // with the stores made every store wait for the previous ones).
+      float bvs[WN];
 #pragma unroll
       for (int j = 0; j < WN; ++j) {
         const int n = TILE_N * (tw + j) + c16;
-        if (n >= p.N) continue;
-        const float bv = bias_at(p, n);
+        bvs[j] = n < p.N ? bias_at(p, n) : 0.f;
+      }
+      wait_vmcnt<0>();
 #pragma unroll
-        for (int t = 0; t < WM; ++t)
+      for (int t = 0; t < WM; ++t) {
+        int drow[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int r = m0 + 16 * t + 4 * quad + i;
-            if (r < row_end) store_c<DT>(p.c, dst_row(r) * p.ldc + n, acc[t][j][i] + bv);
-          }
+        for (int i = 0; i < 4; ++i) {
+          const int r = m0 + 16 * t + 4 * quad + i;
+          drow[i] = r < row_end ? static_cast<int>(dst_row(r)) : -1;
+        }
+        if constexpr (MOE) wait_vmcnt<0>();
+#pragma unroll
+        for (int j = 0; j < WN; ++j) {
+          const int n = TILE_N * (tw + j) + c16;
+          if (n >= p.N) continue;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (drow[i] >= 0) store_c<DT>(p.c, static_cast<int64_t>(drow[i]) * p.ldc + n, acc[t][j][i] + bvs[j]);
+        }
       }
     } else {
       float *part = p.partials + static_cast<int64_t>(blockIdx.z) * p.M * p.N;
