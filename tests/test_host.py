@@ -232,3 +232,27 @@ def test_planner_takes_stream_mfma_for_small_batches():
     assert f(16, 4096, 4096, 32, 0, 0) == 0  # 256 tiles: whole tiles are even
     # A narrow layer (64 tiles) runs two workgroups per tile over global rows.
     assert f(8, 1024, 5120, 32, 1, 0) == cells + 8 * 5120 * 2
+
+
+def test_conv_tile_prepare_rejects_bad_arguments():
+    """The tile-layout prepare entry points check pointers, shapes and dtypes
+    before they launch anything (no device needed for these calls)."""
+    from onecomp_runtime import _hip
+
+    lib = _hip.lib()
+    F16, BF16, F32 = _hip.OC_DTYPE_F16, _hip.OC_DTYPE_BF16, _hip.OC_DTYPE_F32
+    p = 1 << 12  # a non-NULL, 16-byte aligned stand-in: never dereferenced on these paths
+    # oc_rtn_tile_prepare(qweight, N, row_bytes, K, scales, zeros, dtype, G, qt, sz, fast, stream)
+    assert lib.oc_rtn_tile_prepare(None, 16, 64, 128, p, p, F16, 4, p, p, p, None) == _hip.OC_ERR_INVALID_ARGUMENT
+    assert lib.oc_rtn_tile_prepare(p, 16, 64, 120, p, p, F16, 4, p, p, p, None) == _hip.OC_ERR_SHAPE  # K % 32
+    assert lib.oc_rtn_tile_prepare(p, 16, 64, 128, p, p, F16, 8, p, p, p, None) == _hip.OC_ERR_SHAPE  # 16-row groups
+    assert lib.oc_rtn_tile_prepare(p, 16, 32, 128, p, p, F16, 4, p, p, p, None) == _hip.OC_ERR_SHAPE  # short rows
+    assert lib.oc_rtn_tile_prepare(p, 16, 64, 128, p, p, F32, 4, p, p, p, None) == _hip.OC_ERR_INVALID_ARGUMENT
+    assert "16-bit" in _hip.last_error()
+    # oc_rtn_tile_prepare_t(qweight, K, row_bytes, N, scales, zeros, scale_dtype, G, x_dtype, qt, szt, fast, stream)
+    assert lib.oc_rtn_tile_prepare_t(p, 64, 64, 128, p, p, F16, 4, BF16, None, p, p, None) == \
+        _hip.OC_ERR_INVALID_ARGUMENT
+    assert lib.oc_rtn_tile_prepare_t(p, 48, 64, 128, p, p, F16, 4, BF16, p, p, p, None) == _hip.OC_ERR_SHAPE  # K
+    assert lib.oc_rtn_tile_prepare_t(p, 64, 64, 128, p, p, F16, 16, BF16, p, p, p, None) == _hip.OC_ERR_SHAPE  # gs 8
+    assert lib.oc_rtn_tile_prepare_t(p, 64, 64, 128, p, p, F16, 4, F32, p, p, p, None) == \
+        _hip.OC_ERR_INVALID_ARGUMENT
