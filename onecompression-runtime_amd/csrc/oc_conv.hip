@@ -129,28 +129,85 @@ __global__ __launch_bounds__(256) void conv1d_epilogue_tile_kernel(const float *
                                                                       : 0.f;
   const int64_t mn = static_cast<int64_t>(rows) * N;
   constexpr int U = EP_R * EP_N / 256;
-  int64_t e[U];
-  float v[U];
+  if ((N & 3) == 0) {
+    // 16-byte loads of 4 columns (N % 4 == 0: a run never leaves its row).
+    constexpr int U4 = U / 4, C4 = EP_N / 4;
+    int64_t e[U4];
+    float4 v[U4];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int i = threadIdx.x + 256 * u, rr = i / EP_N, nn = i % EP_N;
-    e[u] = rb + rr < rows && nb + nn < N ? static_cast<int64_t>(rb + rr) * N + nb + nn : -1;
-    v[u] = 0.f;
-  }
-  for (int sp = 0; sp < ksplit; ++sp) {
+    for (int u = 0; u < U4; ++u) {
+      const int i = threadIdx.x + 256 * u, rr = i / C4, c = 4 * (i % C4);
+      e[u] = rb + rr < rows && nb + c < N ? static_cast<int64_t>(rb + rr) * N + nb + c : -1;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    for (int sp = 0; sp < ksplit; ++sp) {
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (e[u] >= 0) v[u] += part[sp * mn + e[u]];
-  }
+      for (int u = 0; u < U4; ++u)
+        if (e[u] >= 0) {
+          const float4 t = *reinterpret_cast<const float4 *>(part + sp * mn + e[u]);
+          v[u].x += t.x;
+          v[u].y += t.y;
+          v[u].z += t.z;
+          v[u].w += t.w;
+        }
+    }
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int i = threadIdx.x + 256 * u;
-    tile[i / EP_N][i % EP_N] = v[u];
+    for (int u = 0; u < U4; ++u) {
+      const int i = threadIdx.x + 256 * u, rr = i / C4, c = 4 * (i % C4);
+      tile[rr][c] = v[u].x;
+      tile[rr][c + 1] = v[u].y;
+      tile[rr][c + 2] = v[u].z;
+      tile[rr][c + 3] = v[u].w;
+    }
+  } else {
+    int64_t e[U];
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = threadIdx.x + 256 * u, rr = i / EP_N, nn = i % EP_N;
+      e[u] = rb + rr < rows && nb + nn < N ? static_cast<int64_t>(rb + rr) * N + nb + nn : -1;
+      v[u] = 0.f;
+    }
+    for (int sp = 0; sp < ksplit; ++sp) {
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (e[u] >= 0) v[u] += part[sp * mn + e[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = threadIdx.x + 256 * u;
+      tile[i / EP_N][i % EP_N] = v[u];
+    }
   }
   __syncthreads();
   const int64_t ra = r0 + rb;
   const int64_t b0 = ra / T;
   const int t0 = static_cast<int>(ra - b0 * T);
+  if ((T & 1) == 0) {
+    // Pairs of positions as 4-byte stores: T even keeps t0 (ra is even) and
+    // every pair's first position even, so a pair never leaves its batch row.
+    uint32_t *y32 = static_cast<uint32_t *>(y);
+#pragma unroll
+    for (int u = 0; u < U / 2; ++u) {
+      const int i = threadIdx.x + 256 * u, nn = i / (EP_R / 2), rr = 2 * (i % (EP_R / 2)), n = nb + nn;
+      if (rb + rr >= rows || n >= N) continue;
+      float v0 = tile[rr][nn], v1 = tile[rr + 1][nn];
+      if (bias) {
+        v0 += bs[nn];
+        v1 += bs[nn];
+      }
+      int t = t0 + rr;
+      int64_t b = b0;
+      while (t >= T) {
+        t -= T;
+        ++b;
+      }
+      const int64_t o = (b * N + n) * T + t;
+      if (rb + rr + 1 < rows) y32[o >> 1] = pack2<DT>(v0, v1);
+      else store_c<DT>(y, o, v0);
+    }
+    return;
+  }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int i = threadIdx.x + 256 * u, nn = i / EP_R, rr = i % EP_R, n = nb + nn;
@@ -336,11 +393,9 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
   }
   __syncthreads();
   const int dmax = (k - 1) * dilation;
-  for (int i = threadIdx.x; i < CT_T * CT_O; i += 256) {
-    const int ol = i / CT_T, t = t0 + (i - ol * CT_T), o = o0 + ol;
-    if (t >= t_hi || o >= O) continue;
-    // Taps kk ascending = input positions j descending (j * stride = t + padding - kk * dilation); only the
-    // positions that are whole multiples are visited.
+  // Taps kk ascending = input positions j descending (j * stride = t + padding - kk * dilation); only the
+  // positions that are whole multiples are visited.
+  auto taps = [&](int t, int ol) {
     const int base = t + padding;
     float v = 0.f;
     for (int j = floor_div(base, stride); j >= jlo; --j) {
@@ -354,6 +409,12 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
       }
       v += zs[(j - jlo) * WS + ol * k + kk];
     }
+    return v;
+  };
+  for (int i = threadIdx.x; i < CT_T * CT_O; i += 256) {
+    const int ol = i / CT_T, t = t0 + (i - ol * CT_T), o = o0 + ol;
+    if (t >= t_hi || o >= O) continue;
+    float v = taps(t, ol);
     if constexpr (FINAL) {
       if (bias) v += bs[ol];
       store_c<DT>(y, static_cast<int64_t>(o) * Lout + t, v);
