@@ -337,6 +337,10 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
   constexpr int U = 8;
   if ((N & 3) == 0) {
     const int W4 = W >> 2, tot4 = total >> 2;
+    // (row, column) of element i = threadIdx.x + 256 n, advanced by 256
+    // elements per step (one division per thread, none per element)
+    const int dq = 256 / W4, dr = 256 - dq * W4;
+    int jj = static_cast<int>(threadIdx.x) / W4, c4 = static_cast<int>(threadIdx.x) - jj * W4;
     for (int i0 = threadIdx.x; i0 < tot4; i0 += U * 256) {
       int64_t e[U];
       int li[U];
@@ -344,13 +348,19 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int i = i0 + u * 256;
-        const int jj = i / W4, c = 4 * (i - jj * W4);
+        const int c = 4 * c4;
         const int j = jlo + jj - j0;
         li[u] = (jj * WS + c) >> 2;
         e[u] = i < tot4 && j >= 0 && j < rows && c < wlim
                    ? static_cast<int64_t>(j) * N + static_cast<int64_t>(o0) * k + c
                    : -1;
         v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        jj += dq;
+        c4 += dr;
+        if (c4 >= W4) {
+          c4 -= W4;
+          ++jj;
+        }
       }
       for (int sp = 0; sp < ksplit; ++sp) {
 #pragma unroll
@@ -393,33 +403,41 @@ __global__ __launch_bounds__(256) void col2im_tile_kernel(const float *__restric
   }
   __syncthreads();
   const int dmax = (k - 1) * dilation;
-  // Taps kk ascending = input positions j descending (j * stride = t + padding - kk * dilation); only the
-  // positions that are whole multiples are visited.
-  auto taps = [&](int t, int ol) {
-    const int base = t + padding;
-    float v = 0.f;
-    for (int j = floor_div(base, stride); j >= jlo; --j) {
-      const int d = base - j * stride;  // kk * dilation
-      if (d > dmax || j < j0) break;
-      if (j >= j0 + rows) continue;
-      int kk = d;
-      if (dilation != 1) {
-        if (d % dilation != 0) continue;
-        kk = d / dilation;
-      }
-      v += zs[(j - jlo) * WS + ol * k + kk];
+  // A thread keeps one position t of the tile and takes NO of its channels
+  // (ol = olb, olb + 2, ...): the taps depend on t only, so they are walked
+  // once for all NO sums. Taps kk ascending = input positions j descending
+  // (j * stride = t + padding - kk * dilation); only the positions that are
+  // whole multiples are visited.
+  static_assert(CT_T * 2 == 256, "two channel rows per pass of 256 threads");
+  constexpr int NO = CT_O / 2;
+  const int tl = static_cast<int>(threadIdx.x) % CT_T, olb = static_cast<int>(threadIdx.x) / CT_T;
+  const int t = t0 + tl;
+  if (t >= t_hi) return;
+  float v[NO];
+#pragma unroll
+  for (int u = 0; u < NO; ++u) v[u] = 0.f;
+  const int base = t + padding;
+  for (int j = floor_div(base, stride); j >= jlo; --j) {
+    const int d = base - j * stride;  // kk * dilation
+    if (d > dmax || j < j0) break;
+    if (j >= j0 + rows) continue;
+    int kk = d;
+    if (dilation != 1) {
+      if (d % dilation != 0) continue;
+      kk = d / dilation;
     }
-    return v;
-  };
-  for (int i = threadIdx.x; i < CT_T * CT_O; i += 256) {
-    const int ol = i / CT_T, t = t0 + (i - ol * CT_T), o = o0 + ol;
-    if (t >= t_hi || o >= O) continue;
-    float v = taps(t, ol);
+    const float *zr = zs + (j - jlo) * WS + olb * k + kk;
+#pragma unroll
+    for (int u = 0; u < NO; ++u) v[u] += zr[2 * u * k];
+  }
+#pragma unroll
+  for (int u = 0; u < NO; ++u) {
+    const int ol = olb + 2 * u, o = o0 + ol;
+    if (o >= O) break;
     if constexpr (FINAL) {
-      if (bias) v += bs[ol];
-      store_c<DT>(y, static_cast<int64_t>(o) * Lout + t, v);
+      store_c<DT>(y, static_cast<int64_t>(o) * Lout + t, bias ? v[u] + bs[ol] : v[u]);
     } else {
-      acc[static_cast<int64_t>(o) * Lout + t] += v;
+      acc[static_cast<int64_t>(o) * Lout + t] += v[u];
     }
   }
 }
