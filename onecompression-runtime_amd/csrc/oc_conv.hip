@@ -44,11 +44,13 @@ __global__ __launch_bounds__(256) void im2col_kernel(const uint16_t *__restrict_
 
 // The same rows by tiles of I2C_TR output rows x I2C_CB input channels: the
 // tile's input window (channels ci0.., positions t0 * stride - pad_left ..,
-// W of them, zeros outside [0, L)) is read once into LDS with consecutive
-// positions per thread, then every output row's I2C_CB * k columns are
-// written as 16-byte chunks. A tile whose rows span two batch rows reads its
-// values from global memory instead.
-constexpr int I2C_TR = 64, I2C_CB = 32;
+// W of them, zeros outside [0, L)) is read once into LDS (a wave reads 64
+// consecutive positions of each of its 8 channels per pass, the 8 loads in
+// flight together), then every output row's I2C_CB * k columns are written as
+// 16-byte chunks. A tile whose rows span two batch rows reads its values from
+// global memory instead. 128 rows per tile: the window rows (W positions of
+// a channel) span fewer partial cache lines than at 64.
+constexpr int I2C_TR = 128, I2C_CB = 32;
 inline int i2c_window(int k, int stride, int dilation) { return (I2C_TR - 1) * stride + (k - 1) * dilation + 1; }
 
 __global__ __launch_bounds__(256) void im2col_tile_kernel(const uint16_t *__restrict__ x, int C, int L, int k,
@@ -63,9 +65,19 @@ __global__ __launch_bounds__(256) void im2col_tile_kernel(const uint16_t *__rest
   if (one_batch) {
     const int p0 = t0 * stride - pad_left;
     const uint16_t *xb = x + (static_cast<int64_t>(b0) * C + ci0) * L;
-    for (int i = threadIdx.x; i < I2C_CB * W; i += blockDim.x) {
-      const int c = i / W, pos = p0 + (i - c * W);
-      win[i] = pos >= 0 && pos < L ? xb[static_cast<int64_t>(c) * L + pos] : static_cast<uint16_t>(0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int CPW = I2C_CB / 4;  // channels per wave
+    for (int q0 = 0; q0 < W; q0 += 64) {
+      const int q = q0 + lane, pos = p0 + q;
+      const bool in = q < W && pos >= 0 && pos < L;
+      uint16_t v[CPW];
+#pragma unroll
+      for (int u = 0; u < CPW; ++u)
+        v[u] = in ? xb[static_cast<int64_t>(wave + 4 * u) * L + pos] : static_cast<uint16_t>(0);
+      if (q < W) {
+#pragma unroll
+        for (int u = 0; u < CPW; ++u) win[(wave + 4 * u) * W + q] = v[u];
+      }
     }
     __syncthreads();
   }
