@@ -630,7 +630,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}, WORLD_SIZE={world}); "
-              "this workload does not shard across GPUs in this build", file=sys.stderr)
+              "this package runs the workload on one GPU", file=sys.stderr)
         return 2
 
     import torch

@@ -11,7 +11,7 @@
 - :class:`Dsv4PackedLinear` - DeepSeek-V4 QEP int4/int2 layers, host-resident
   experts staged to the device per call.
 - :class:`GemLiteInt4Linear` / :func:`gemlite_available` - import-compatible
-  names only (GemLite is never available on this build).
+  names only (GemLite, a Triton library, is never available on this HIP package).
 """
 from __future__ import annotations
 

@@ -1,7 +1,7 @@
 """GemLite names kept for import compatibility.
 
 GemLite is a Triton library tuned for NVIDIA GPUs (reference:
-layers/gemlite_int4_linear.py:20-98); this build dispatches no Triton code,
+layers/gemlite_int4_linear.py:20-98); this package dispatches no Triton code,
 so it is never available and the GemLite backends raise as the reference does
 when the package is missing (backend.py:116-131).
 """
