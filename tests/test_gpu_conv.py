@@ -111,10 +111,12 @@ def test_conv1d_large_m_kernel(case, monkeypatch):
     say(f"conv1d large-M kernel case {case}")
     mod0 = PackedInt4Conv1d(cin, cout, k, qweight=torch.from_numpy(q), scales=s_t, zeros=z_t, cols=cols,
                             pad_mode="none").to(DEV)
-    y1 = mod0(x.to(DEV))
-    assert mod0._tile_cache is not None and mod0._tile_cache[3] == (1, 1)
-    ref1 = O.conv1d(np32(x), w, None, 1, 1, 0, T, "bf16")
-    assert np.array_equal(bits16(y1), oracle_bits(ref1, torch.bfloat16))
+    for tdt, odt in ((torch.bfloat16, "bf16"), (torch.float16, "f16")):
+        y1 = mod0(x.to(tdt).to(DEV))
+        assert mod0._tile_cache is not None and mod0._tile_cache[3] == (1, 1)
+        wo = O.rtn_dequant(q, s32, z32, cols, cout, odt).reshape(cout, cin, k)
+        ref1 = O.conv1d(np32(x), wo, None, 1, 1, 0, T, odt)
+        assert np.array_equal(bits16(y1), oracle_bits(ref1, tdt)), odt
     yr = mod(xr.to(DEV))
     assert_gemm_close(yr, ref, f"conv1d large-M case {case}")
     monkeypatch.setenv("ONECOMP_HIP_CONV_WIDE", "0")
