@@ -566,14 +566,32 @@ __global__ __launch_bounds__(256) void rtnt_tile_rows_kernel(const uint16_t *__r
 // Large-M conv GEMM (the tiled RTN kernel below this many rows per chunk).
 constexpr int WIDE_CONV_MIN_ROWS = 1024;
 
-// K slices of the large-M kernel for a rows x N x K chunk: enough 256 x 192
-// workgroups to fill the compute units, each slice 16 K steps or more.
-int wide_conv_ksplit(int rows, int N, int K, int *kps) {
-  const int KS = K / 32;
-  const int wgs = ((N + 191) / 192) * ((rows + 255) / 256);
-  int ks = std::max(1, std::min(device_cus() / std::max(1, wgs), KS / 16));
-  *kps = (KS + ks - 1) / ks;
-  return (KS + *kps - 1) / *kps;
+// Large-M plan of a rows x N x K chunk: K slices (each 16 K steps or more)
+// enough to fill the compute units with 256-row workgroups, for column
+// blocks of 64 wn; *wn (when given) gets the block width, 192 or 128, whose
+// grid keeps the most CUs busy on useful columns (ties: 192); without wn,
+// 192 only.
+int wide_conv_ksplit(int rows, int N, int K, int *kps, int *wn = nullptr) {
+  const int KS = K / 32, cus = device_cus();
+  double best = -1.0;
+  int best_ks = 1, best_wn = 3;
+  for (int w : {3, 2}) {
+    if (w == 2 && !wn) continue;
+    const int nbn = (N + 64 * w - 1) / (64 * w), base = nbn * ((rows + 255) / 256);
+    const int ks = std::max(1, std::min(cus / std::max(1, base), KS / 16));
+    const int kp = (KS + ks - 1) / ks, ksr = (KS + kp - 1) / kp;
+    const int64_t wgs = static_cast<int64_t>(base) * ksr;
+    const double fill = static_cast<double>(wgs) / (static_cast<double>((wgs + cus - 1) / cus) * cus);
+    const double useful = static_cast<double>(N) / (static_cast<double>(nbn) * 64 * w);
+    if (fill * useful > best + 0.02) {
+      best = fill * useful;
+      best_ks = ksr;
+      best_wn = w;
+      *kps = kp;
+    }
+  }
+  if (wn) *wn = best_wn;
+  return best_ks;
 }
 
 // Rows per chunk: a bounded workspace (activation rows plus fp32 partials),
@@ -595,7 +613,10 @@ int chunk_rows(int64_t total, int K, int N) {
 size_t chunk_bytes(int rows, int K, int N) {
   int wm, wn, kg, ksplit, kps;
   plan_tiled(rows, N, K, &wm, &wn, &kg, &ksplit, &kps);
-  if (rows >= WIDE_CONV_MIN_ROWS) ksplit = std::max(ksplit, wide_conv_ksplit(rows, N, K, &kps));
+  if (rows >= WIDE_CONV_MIN_ROWS) {
+    int wn;
+    ksplit = std::max(ksplit, wide_conv_ksplit(rows, N, K, &kps, &wn));
+  }
   const size_t a = (static_cast<size_t>(rows) * K * 2 + 255) / 256 * 256;
   return a + static_cast<size_t>(ksplit) * rows * N * sizeof(float);
 }
@@ -786,8 +807,9 @@ int oc_rtn_conv1d_prepared(const void *x, int32_t x_dtype, int32_t B, int32_t C_
       p.gshift = ilog2_exact(gs / 32);
       p.partials = part;
       p.out_f32 = 1;
-      p.ksplit = wide_conv_ksplit(rows, C_out, K, &p.ksteps_per_split);
-      launch_rtn_wide(p, x_dtype, scale_dtype, s);
+      int wn;
+      p.ksplit = wide_conv_ksplit(rows, C_out, K, &p.ksteps_per_split, &wn);
+      launch_rtn_wide(p, x_dtype, scale_dtype, wn, s);
       ksplit = p.ksplit;
     } else {
       ksplit = chunk_gemm(a, x_dtype, rows, K, qweight, row_bytes, scales, scale_dtype, zeros, zero_dtype, K / G, G,
@@ -913,8 +935,9 @@ int oc_rtn_conv_transpose1d_prepared(const void *x, int32_t x_dtype, int32_t B, 
         p.gshift = 0;
         p.partials = part;
         p.out_f32 = 1;
-        p.ksplit = wide_conv_ksplit(rows, N, C_in, &p.ksteps_per_split);
-        launch_rtnt_wide(p, x_dtype, s);
+        int wn;
+        p.ksplit = wide_conv_ksplit(rows, N, C_in, &p.ksteps_per_split, &wn);
+        launch_rtnt_wide(p, x_dtype, wn, s);
         ksplit = p.ksplit;
       } else {
         ksplit = chunk_gemm(a, x_dtype, rows, C_in, qweight_t, C_in / 2, scales_t, scale_dtype, zeros_t, scale_dtype,

@@ -225,11 +225,12 @@ void launch_rows_gemv(const GemmParams &p, int x_dtype, int fmt, hipStream_t s);
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);
 // RTN tiles (oc_rtn_tile_prepare) on the large-M kernel into fp32 partials
 // [p.ksplit][M][N] (p.out_f32 = 1, p.partials); group steps a power of two
-// (p.gshift >= 0), N % 8 == 0, every group fast-dequant eligible.
-void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, hipStream_t s);
+// (p.gshift >= 0), N % 8 == 0, every group fast-dequant eligible; column
+// blocks of 64 wn (wn = 2 or 3).
+void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s);
 // Transposed-group RTN tiles (oc_rtn_tile_prepare_t, row words in a_dtype)
 // on the large-M kernel into fp32 partials, as launch_rtn_wide.
-void launch_rtnt_wide(const GemmParams &p, int a_dtype, hipStream_t s);
+void launch_rtnt_wide(const GemmParams &p, int a_dtype, int wn, hipStream_t s);
 
 // Decode GEMV over work items of T tiles x S K steps (oc_gemv.hip). K is split
 // into ksplit = ceil(KS / S) ranges; with ksplit > 1 the launch needs

@@ -53,20 +53,22 @@ constexpr int WIDE_NS = 4;  // LDS ring depth (stages), default
 //   WN = 3: 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 the scales
 //           (lanes 0-23) to S; 4-byte DMA: wave 0 the zero words (lanes 0-23),
 //           waves 1-3 a pad.
-//   RTN (WN = 3): 16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 a pad
-//           (Z, 1 KB); 4-byte DMA: waves 0-2 copy the scale|zero words of
-//           tiles 4w..4w+3 to S + 64w (16 words per tile), wave 3 a pad.
-//   RTN_T (WN = 3): the 32 row words of each tile and K step at S + 32 tile:
-//           16-byte DMA: waves 0-2 copy tiles 4w..4w+3, wave 3 the row
-//           words of tiles 0-7; 4-byte DMA: waves 0-1 those of tiles
-//           8+2w, 9+2w, waves 2-3 a pad.
+//   RTN (WN = 3 or 2): 16-byte DMA: waves w < WN copy tiles 4w..4w+3, the
+//           others a pad (Z, 1 KB); 4-byte DMA: waves w < WN copy the
+//           scale|zero words of tiles 4w..4w+3 to S + 64w (16 words per
+//           tile), the others a pad.
+//   RTN_T (WN = 3 or 2): the 32 row words of each tile and K step at
+//           S + 32 tile: 16-byte DMA: waves w < WN copy tiles 4w..4w+3,
+//           wave WN the row words of tiles 0-7, a wave past it a pad (Z,
+//           1 KB); 4-byte DMA (WN = 3): waves 0-1 the row words of tiles
+//           8+2w, 9+2w, the others (and every wave at WN = 2) a pad.
 template <int WN, int FMT = FMT_GPTQ>
 struct WideLayout {
   static constexpr int TILES = 4 * WN;
   static constexpr int W = 0;
   static constexpr int S = 256 * WN;
   static constexpr int Z = S + (FMT == FMT_RTN ? 16 * TILES : FMT == FMT_RTN_T ? 32 * TILES : WN == 4 ? 128 : 256);
-  static constexpr int P = Z + (FMT == FMT_RTN ? 256 : 64);
+  static constexpr int P = Z + (FMT == FMT_RTN || FMT == FMT_RTN_T ? 256 : 64);
   static constexpr int DW = P + 64;
 };
 
@@ -98,7 +100,7 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   constexpr bool RTNT = FMT == FMT_RTN_T;
   constexpr bool RTN = FMT == FMT_RTN || RTNT;  // K slices, fp32 partials, wave 3's 16-byte job
   static_assert(NS == 4 || NS == 6, "ring depth");
-  static_assert(FMT == FMT_GPTQ || (RTN && WN == 3), "formats");
+  static_assert(FMT == FMT_GPTQ || (RTN && (WN == 3 || WN == 2)), "formats");
   constexpr int BM = 256;
   constexpr int AST = BM * 4;  // uint4 per activation slot
   constexpr int DMA = 6;       // DMA instructions per wave and stage
@@ -168,12 +170,12 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
   uint32_t vo_x, vo_y;
   int x_kind, y_kind;  // 0: words, 1: scales, 2: zeros, 3: pad (soffset selector)
   int x_dst, y_dst;    // dword offsets in the slot
-  if (RTNT && wave == 3) {
+  if (RTNT && wave == WN) {
     rs_x = rs_s;
     vo_x = static_cast<uint32_t>(tile_at(lane >> 3)) * p.K_phys * 4 + 16 * (lane & 7);
     x_kind = 5;
     x_dst = L::S;
-  } else if (RTN && wave == 3) {
+  } else if (RTN && wave >= WN) {
     rs_x = rs_q;
     vo_x = OOB_OFFSET;
     x_kind = 3;
@@ -190,17 +192,18 @@ __global__ __launch_bounds__(256, 1) void gemm_wide_kernel(GemmParams p) {
     x_dst = L::W + 256 * wave;
   }
   if (RTNT) {
+    const bool job = WN == 3 && wave < 2;
     rs_y = rs_s;
-    vo_y = wave < 2 ? static_cast<uint32_t>(tile_at(8 + 2 * wave + (lane >> 5))) * p.K_phys * 4 + 4 * (lane & 31)
-                    : OOB_OFFSET;
-    y_kind = wave < 2 ? 5 : 3;
-    y_dst = wave < 2 ? L::S + 256 + 64 * wave : L::P;
+    vo_y = job ? static_cast<uint32_t>(tile_at(8 + 2 * wave + (lane >> 5))) * p.K_phys * 4 + 4 * (lane & 31)
+               : OOB_OFFSET;
+    y_kind = job ? 5 : 3;
+    y_dst = job ? L::S + 256 + 64 * wave : L::P;
   } else if (RTN) {
     rs_y = rs_s;
-    vo_y = wave < 3 ? static_cast<uint32_t>(tile_at(4 * wave + (lane >> 4))) * p.G * 64 + 4 * (lane & 15)
-                    : OOB_OFFSET;
-    y_kind = wave < 3 ? 4 : 3;
-    y_dst = wave < 3 ? L::S + 64 * wave : L::P;
+    vo_y = wave < WN ? static_cast<uint32_t>(tile_at(4 * wave + (lane >> 4))) * p.G * 64 + 4 * (lane & 15)
+                     : OOB_OFFSET;
+    y_kind = wave < WN ? 4 : 3;
+    y_dst = wave < WN ? L::S + 64 * wave : L::P;
   } else if (WN == 4 && wave < 2) {
     rs_y = rs_s;
     vo_y = static_cast<uint32_t>(tile_at(8 * wave + (lane >> 3))) * p.G * 32 + 4 * (lane & 7);
@@ -486,34 +489,36 @@ static void launch_wide_d(const GemmParams &p, int wn, hipStream_t s) {
 // RTN tiles (WN = 3, 4-slot ring) into fp32 partials: p.ksplit slices of
 // p.ksteps_per_split K steps each.
 template <int DT, int SDT>
-static void launch_rtn_wide_t(const GemmParams &p, hipStream_t s) {
+static void launch_rtn_wide_t(const GemmParams &p, int wn, hipStream_t s) {
   static const int ns = env_int("ONECOMP_HIP_RTN_WIDE_NS", WIDE_NS);
-  const int nbn = (p.N + 191) / 192, nbm = (p.M + 255) / 256;
+  const int nbn = (p.N + 64 * wn - 1) / (64 * wn), nbm = (p.M + 255) / 256;
   const dim3 g(nbn * nbm * p.ksplit);
-  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 6, FMT_RTN>), g, dim3(256), 0, s, p);
+  if (wn == 2) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 2, 4, FMT_RTN>), g, dim3(256), 0, s, p);
+  else if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 6, FMT_RTN>), g, dim3(256), 0, s, p);
   else hipLaunchKernelGGL((gemm_wide_kernel<DT, SDT, 3, 4, FMT_RTN>), g, dim3(256), 0, s, p);
 }
 
 template <int DT>
-static void launch_rtnt_wide_t(const GemmParams &p, hipStream_t s) {
+static void launch_rtnt_wide_t(const GemmParams &p, int wn, hipStream_t s) {
   static const int ns = env_int("ONECOMP_HIP_RTN_WIDE_NS", WIDE_NS);
-  const int nbn = (p.N + 191) / 192, nbm = (p.M + 255) / 256;
+  const int nbn = (p.N + 64 * wn - 1) / (64 * wn), nbm = (p.M + 255) / 256;
   const dim3 g(nbn * nbm * p.ksplit);
-  if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 3, 6, FMT_RTN_T>), g, dim3(256), 0, s, p);
+  if (wn == 2) hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 2, 4, FMT_RTN_T>), g, dim3(256), 0, s, p);
+  else if (ns == 6) hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 3, 6, FMT_RTN_T>), g, dim3(256), 0, s, p);
   else hipLaunchKernelGGL((gemm_wide_kernel<DT, DT, 3, 4, FMT_RTN_T>), g, dim3(256), 0, s, p);
 }
 
-void launch_rtnt_wide(const GemmParams &p, int a_dtype, hipStream_t s) {
-  if (a_dtype == OC_DTYPE_BF16) launch_rtnt_wide_t<OC_DTYPE_BF16>(p, s);
-  else launch_rtnt_wide_t<OC_DTYPE_F16>(p, s);
+void launch_rtnt_wide(const GemmParams &p, int a_dtype, int wn, hipStream_t s) {
+  if (a_dtype == OC_DTYPE_BF16) launch_rtnt_wide_t<OC_DTYPE_BF16>(p, wn, s);
+  else launch_rtnt_wide_t<OC_DTYPE_F16>(p, wn, s);
 }
 
-void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, hipStream_t s) {
+void launch_rtn_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s) {
   const bool bf = a_dtype == OC_DTYPE_BF16, sbf = scale_dtype == OC_DTYPE_BF16;
-  if (bf && sbf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, s);
-  else if (bf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_F16>(p, s);
-  else if (sbf) launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_BF16>(p, s);
-  else launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_F16>(p, s);
+  if (bf && sbf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_BF16>(p, wn, s);
+  else if (bf) launch_rtn_wide_t<OC_DTYPE_BF16, OC_DTYPE_F16>(p, wn, s);
+  else if (sbf) launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_BF16>(p, wn, s);
+  else launch_rtn_wide_t<OC_DTYPE_F16, OC_DTYPE_F16>(p, wn, s);
 }
 
 void launch_gptq_wide(const GemmParams &p, int a_dtype, int scale_dtype, int wn, hipStream_t s) {

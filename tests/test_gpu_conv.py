@@ -71,10 +71,11 @@ def test_conv1d_one_hot_bit_exact_and_random(case):
     assert_gemm_close(mod_b(xr.to(DEV)), ref, f"conv1d case {case}")
 
 
-WIDE_CASES = [  # cin, cout, k, G, scale dtype: chunks of >= 1024 rows on the large-M kernel (K slices: 1, 2, 3)
-    (64, 200, 5, 5, np.float16),
+WIDE_CASES = [  # cin, cout, k, G, scale dtype: chunks of >= 1024 rows on the large-M kernel (K slices: 1, 2, 3;
+    (64, 200, 5, 5, np.float16),  # the last case takes 128-column blocks in 4 slices)
     (256, 200, 4, 8, np.float16),
     (320, 96, 5, 25, "bf16"),
+    (512, 256, 4, 16, np.float16),
 ]
 
 
